@@ -1,0 +1,291 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X backend on BASELINE.json's headline metric.
+
+Default workload: bf16 dense GEMM C = A @ B with
+fp32 accumulation and bf16 output, M = N = K = 8192, A row-major [M,K], B
+column-major (stored [N,K]), A,B ~ Normal(0,1)/sqrt(K) from seeds 1 and 2,
+generated on the GPU. A "step" is one pyc_hip_gemm_dispatch launch over the
+resident operands. Prints ONE JSON line.
+
+    python bench.py [--steps K] [--warmup W] [--workload NAME]
+
+Other workloads (--workload) measure the remaining BASELINE configs for the
+record; they are not the bench line the driver reads by default.
+
+The cpu_baseline leg times the reference's own CPU executor (the C11 engine
+built from the reference sources into oracle/_ref/libpyc_ref.so, through
+pyc_compile_model/pyc_run_model) on a bounded row sample of the same GEMM, or
+the oracle's restatement when that library is absent.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "bf16 GEMM/attention TFLOP/s + % MFMA peak at 1 MI355X; speedup vs CPU executor"
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA (published)
+PEAK_F32_TFLOPS = 157.3     # MI355X dense fp32 MFMA (published)
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E (published)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------- timing helpers
+
+
+def time_launches(torch, launch, steps: int, warmup: int):
+    """Warm up, then time `steps` launches: total bracketed by synchronize, and
+    each launch between HIP events recorded on the stream it runs on."""
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        launch()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for e0, e1 in evs:
+        e0.record(stream)
+        launch()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    per = [e0.elapsed_time(e1) for e0, e1 in evs]
+    return wall_ms / steps, float(np.mean(per)), per
+
+
+def load_traffic(name: str):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
+    scaled by the copy-kernel calibration), committed under profiles/."""
+    p = os.path.join(ROOT, "profiles", f"{name}.traffic.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        return json.load(f).get("hbm_bytes_per_launch")
+
+
+# ---------------------------------------------------------------- CPU baseline
+
+
+def cpu_baseline_gemm(a_rows_f32: np.ndarray, b_kn_f32: np.ndarray, full_flops: float, sample_desc: str):
+    """Time the reference CPU executor on a[rows] @ b (fp32) and scale to the
+    metric's unit (TFLOP/s on the full workload's FLOP count; the per-row cost
+    is constant so throughput extrapolates linearly)."""
+    rows, k = a_rows_f32.shape
+    n = b_kn_f32.shape[1]
+    flops = 2.0 * rows * k * n
+    threads = min(os.cpu_count() or 1, 32)
+    try:
+        from tests import refengine
+        use_ref = refengine.available()
+    except Exception:  # noqa: BLE001
+        use_ref = False
+    out = None
+    if use_ref:
+        os.environ["PYC_NUM_THREADS"] = str(threads)
+        model = refengine.matmul_model(rows, k, n)
+        try:
+            model.run([a_rows_f32, b_kn_f32], [(rows, n)])  # warm (page-in)
+            t0 = time.perf_counter()
+            st, (out,), _ = model.run([a_rows_f32, b_kn_f32], [(rows, n)])
+            dt = time.perf_counter() - t0
+        finally:
+            model.close()
+            os.environ.pop("PYC_NUM_THREADS", None)
+        assert st == 0
+        kind = "reference"
+    else:
+        import oracle
+        t0 = time.perf_counter()
+        out = oracle.matmul_f32(a_rows_f32, b_kn_f32, threads)
+        dt = time.perf_counter() - t0
+        kind = "port"
+    tflops = flops / dt / 1e12
+    return {
+        "value": tflops,
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": kind,
+        "sample": f"{sample_desc}; {flops / 1e9:.1f} GFLOP in {dt:.2f} s, extrapolated linearly "
+                  f"(full job {full_flops / 1e12:.3f} TFLOP -> {full_flops / flops * dt:.0f} s)",
+    }, out
+
+
+# ---------------------------------------------------------------- workloads
+
+
+def wl_gemm_bf16(torch, args):
+    import pyc_amd
+    M = N = K = 8192
+    g1 = torch.Generator(device="cuda").manual_seed(1)
+    g2 = torch.Generator(device="cuda").manual_seed(2)
+    A = (torch.randn((M, K), generator=g1, device="cuda") / np.sqrt(K)).to(torch.bfloat16)
+    B = (torch.randn((N, K), generator=g2, device="cuda") / np.sqrt(K)).to(torch.bfloat16)
+    Cd = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    sym = args.symbol or "hip_gemm_bf16_nt"
+    launch = lambda: pyc_amd.gemm(sym, A, B, Cd, M, N, K)  # noqa: E731
+    ms_step, ms_kernel, _ = time_launches(torch, launch, args.steps, args.warmup)
+    flops = 2.0 * M * N * K
+    value = flops / (ms_step * 1e-3) / 1e12
+    achieved = flops / (ms_kernel * 1e-3) / 1e12
+    res = {
+        "value": value, "unit": "TFLOP/s", "ms_per_step": ms_step, "dtype": "bf16",
+        "config": {"workload": "gemm_bf16_nt_8192x8192x8192", "kernel": sym, "M": M, "N": N, "K": K,
+                   "layout": "A row-major [M,K], B column-major [N,K], C row-major bf16",
+                   "accumulate": "fp32", "seeds": [1, 2], "init": "Normal(0,1)/sqrt(K)"},
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / PEAK_BF16_TFLOPS,
+                     "traffic": load_traffic("gemm_bf16_nt_8192"),
+                     "kernel_ms": ms_kernel, "algorithmic_flop_per_launch": flops,
+                     "algorithmic_bytes_per_launch": 3 * M * N * 2},
+    }
+    if not args.no_cpu:
+        import oracle
+        rows = np.arange(0, M, M // args.cpu_rows)[: args.cpu_rows]
+        ridx = torch.from_numpy(rows).cuda()
+        a_rows = A[ridx].float().cpu().numpy()
+        b_kn = np.ascontiguousarray(B.float().cpu().numpy().T)
+        cpu, out = cpu_baseline_gemm(a_rows, b_kn, flops,
+                                     f"{len(rows)} of {M} rows of the 8192^3 GEMM, fp32 executor on the "
+                                     "exactly decoded bf16 operands")
+        res["cpu_baseline"] = cpu
+        got = Cd[ridx].float().cpu().numpy()
+        res["parity_sample_max_rel_err"] = float(np.abs(got - out).max() / np.abs(out).max())
+        res["speedup_vs_cpu"] = value / cpu["value"]
+        del oracle
+    return res
+
+
+def wl_gemm_f32_cfg1(torch, args):
+    import pyc_amd
+    M = N = K = 1024
+    r = np.random.default_rng(0)
+    x = r.uniform(-1, 1, (M, K)).astype(np.float32)
+    w = r.uniform(-1, 1, (K, N)).astype(np.float32)
+    b = r.uniform(-1, 1, N).astype(np.float32)
+    X, W, Bv = (torch.from_numpy(t).cuda() for t in (x, w, b))
+    Y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    epi = pyc_amd.abi.EPI_BIAS | pyc_amd.abi.EPI_RELU
+    launch = lambda: pyc_amd.gemm("hip_gemm_f32_nn_64x64", X, W, Y, M, N, K, bias=Bv, epilogue=epi)  # noqa: E731
+    ms_step, ms_kernel, _ = time_launches(torch, launch, args.steps, args.warmup)
+    flops = 2.0 * M * N * K + 2.0 * M * N
+    value = flops / (ms_step * 1e-3) / 1e12
+    res = {
+        "value": value, "unit": "TFLOP/s", "ms_per_step": ms_step, "dtype": "f32",
+        "config": {"workload": "gemm_f32_bias_relu_1024", "M": M, "N": N, "K": K},
+        "roofline": {"bound": "mfma", "achieved": flops / (ms_kernel * 1e-3) / 1e12, "peak": PEAK_F32_TFLOPS,
+                     "unit": "TFLOP/s", "frac": flops / (ms_kernel * 1e-3) / 1e12 / PEAK_F32_TFLOPS,
+                     "traffic": load_traffic("gemm_f32_cfg1"), "kernel_ms": ms_kernel},
+    }
+    if not args.no_cpu:
+        cpu, out = cpu_baseline_gemm(x, w, flops, "full config-1 GEMM (bias+ReLU not timed)")
+        res["cpu_baseline"] = cpu
+    return res
+
+
+def wl_decode_chain(torch, args):
+    """Config 5: 8 x [x(32x4096) -> W_up(4096x11008, fp8) -> ReLU -> W_down(11008x4096, fp8)],
+    16 launches captured in one hipGraph, replayed."""
+    import pyc_amd
+    L, M, D, F = 8, 32, 4096, 11008
+    g = torch.Generator(device="cuda").manual_seed(9)
+    x = torch.randn((M, D), generator=g, device="cuda").to(torch.bfloat16)
+    layers = []
+    for l in range(L):
+        gl = torch.Generator(device="cuda").manual_seed(10 + l)
+        w_up = torch.randn((D, F), generator=gl, device="cuda") * np.sqrt(2.0 / D)
+        w_dn = torch.randn((F, D), generator=gl, device="cuda") * np.sqrt(2.0 / F)
+        pack = []
+        for w in (w_up, w_dn):  # per-output-column scale, stored [N,K] e4m3fn
+            s = (w.abs().amax(0) / 448.0).clamp_min(1e-30)
+            q = (w / s).t().contiguous().to(torch.float8_e4m3fn).view(torch.uint8)
+            pack += [q, s.float().contiguous()]
+        layers.append(pack)
+        del w_up, w_dn
+    h = torch.empty((M, F), dtype=torch.bfloat16, device="cuda")
+    ys = [torch.empty((M, D), dtype=torch.bfloat16, device="cuda") for _ in range(2)]
+
+    def chain(stream=None):
+        cur = x
+        for l, (qu, su, qd, sd) in enumerate(layers):
+            pyc_amd.w8a16_gemm(cur, qu, su, h, True, stream=stream)
+            pyc_amd.w8a16_gemm(h, qd, sd, ys[l & 1], False, stream=stream)
+            cur = ys[l & 1]
+
+    chain()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        graph.capture_begin()
+        chain(stream=s.cuda_stream)
+        graph.capture_end()
+    torch.cuda.synchronize()
+    ms_step, ms_kernel, _ = time_launches(torch, graph.replay, args.steps, args.warmup)
+    weight_bytes = L * (2 * D * F + 4 * (F + D))
+    bytes_replay = L * (2 * D * F + 4 * F + 4 * D + M * D * 2 + 2 * M * F * 2 + M * D * 2)
+    gbs = bytes_replay / (ms_step * 1e-3) / 1e9
+    return {
+        "value": gbs, "unit": "GB/s", "ms_per_step": ms_step, "dtype": "fp8-e4m3 weights, bf16 activations",
+        "config": {"workload": "decode_w8a16_chain_8x(32x4096x11008)", "replay": "hipGraph", "launches": 16},
+        "roofline": {"bound": "hbm", "achieved": bytes_replay / (ms_kernel * 1e-3) / 1e9, "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": bytes_replay / (ms_kernel * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                     "traffic": None, "kernel_ms": ms_kernel, "algorithmic_bytes_per_replay": bytes_replay,
+                     "weight_bytes": weight_bytes},
+    }
+
+
+WORKLOADS = {"gemm_bf16": wl_gemm_bf16, "gemm_f32_cfg1": wl_gemm_f32_cfg1, "decode_chain": wl_decode_chain}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="gemm_bf16", choices=sorted(WORKLOADS))
+    ap.add_argument("--symbol", default=None, help="GEMM kernel symbol override")
+    ap.add_argument("--cpu-rows", type=int, default=64)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(no collectives); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+    import pyc_amd
+    if not torch.cuda.is_available():
+        print("no HIP device visible", file=sys.stderr)
+        return 1
+    pyc_amd.lib()  # fail loudly if the HIP library is missing
+    info = pyc_amd.device_info()
+    log(f"device {info.gcn_arch.decode()} CUs={info.compute_units} sclk={info.clock_khz / 1e3:.0f} MHz")
+    res = WORKLOADS[args.workload](torch, args)
+    line = {
+        "metric": METRIC, "value": res["value"], "unit": res["unit"], "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": res["dtype"], "data": "synthetic",
+        "config": res["config"], "roofline": res["roofline"],
+    }
+    for k in ("cpu_baseline", "parity_sample_max_rel_err", "speedup_vs_cpu"):
+        if k in res:
+            line[k] = res[k]
+    line["device"] = {"arch": info.gcn_arch.decode(), "cus": info.compute_units,
+                      "sclk_mhz": info.clock_khz / 1e3}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,100 @@
+/* pyc/hip_backend.h — MI355X (gfx950) extensions of the GPU backend ABI.
+ *
+ * These entry points are additions next to the reference ABI in
+ * pyc/cuda_backend.h (reference cuda_backend.h:105-138 defines the
+ * single-head/no-bias family they generalise). All pointers are DEVICE
+ * pointers, stream is a hipStream_t (NULL = the null stream), nothing is
+ * allocated except where a workspace is said to be. Every function returns
+ *   0  success (kernels enqueued),
+ *  -1  unknown symbol or invalid argument (nothing enqueued),
+ *  -2  HIP launch error (hipGetLastError after the launch). */
+#ifndef PYC_HIP_BACKEND_H
+#define PYC_HIP_BACKEND_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* GEMM epilogue flags: applied to the fp32 accumulator before the store. */
+#define PYC_HIP_EPI_NONE 0
+#define PYC_HIP_EPI_BIAS 1 /* out[m,n] += bias[n] (fp32 bias) */
+#define PYC_HIP_EPI_RELU 2 /* out = max(out, 0) after bias */
+
+/* Generalises reference gemm/kernel.cu:151-203 (pyc_cutlass_gemm_dispatch):
+ * C[M,N] = epilogue(alpha * A[M,K] * op(B) + beta * C), fp32 accumulate.
+ * The symbol fixes the element type and B's layout:
+ *   hip_gemm_bf16_nt  bf16  B stored [N,K] (column-major B)
+ *   hip_gemm_bf16_nn  bf16  B stored [K,N]
+ *   hip_gemm_f16_nt / hip_gemm_f16_nn   fp16, same layouts
+ *   hip_gemm_f32_nn / hip_gemm_f32_nt   fp32 (true fp32 MFMA, no TF32)
+ * A and C are row-major. Any M,N,K >= 1. */
+int pyc_hip_gemm_dispatch(
+    const char* symbol,
+    int M, int N, int K,
+    const void* A, const void* B, void* C,
+    float alpha, float beta,
+    const float* bias, int epilogue,
+    void* stream);
+
+/* Generalises reference attention/kernel.cu:95-122 to batch and heads:
+ * O[b,h] = softmax(Q[b,h] K[b,h]^T * scale (+ causal mask)) V[b,h],
+ * Q,K,V,O [B,H,S,D] contiguous (BHSD), fp32 softmax and accumulation.
+ * Symbol "hip_attention_bf16" (bf16) or "hip_attention_f16". D in {64,128}. */
+int pyc_hip_attention_dispatch(
+    const char* symbol,
+    int B, int H, int S, int D, int causal,
+    const void* Q, const void* K, const void* V, void* O,
+    float scale, void* stream);
+
+/* Generalises reference conv2d/kernel.cu:80-112 with a fused epilogue:
+ * y[n,p,q,k] = relu?(bias[k] + sum_{r,s,c} x[n,p*sh-ph+r,q*sw-pw+s,c] w[k,r,s,c]),
+ * x NHWC, w KRSC, y NPQK; out-of-image taps read zero. bias may be NULL.
+ * Symbol "hip_conv2d_bf16" (bf16) or "hip_conv2d_f16". C_in % 8 == 0. */
+int pyc_hip_conv2d_dispatch(
+    const char* symbol,
+    int N, int H, int W, int C_in,
+    int K, int R, int S,
+    int pad_h, int pad_w, int stride_h, int stride_w,
+    const void* x, const void* w, const float* bias, int relu,
+    void* y, void* stream);
+
+/* Weight-only fp8 GEMM for decode (no reference counterpart: the reference
+ * has no fp8 type, reference include/pyc/ir.h:16-23):
+ * Y[M,N] = relu?( (X[M,K] * dequant(Wq)^T)[m,n] * scale[n] )
+ * X bf16 row-major [M,K]; Wq OCP e4m3fn stored [N,K] (each output channel's
+ * K weights contiguous); scale fp32 [N]; Y bf16 [M,N]. 1 <= M <= 32, K % 16 == 0.
+ * Symbol "hip_gemm_w8a16_e4m3". */
+int pyc_hip_w8a16_gemm_dispatch(
+    const char* symbol,
+    int M, int N, int K,
+    const void* X, const void* Wq, const float* scale, int relu,
+    void* Y, void* stream);
+
+/* Device properties the bench and the registry report. */
+typedef struct {
+    char gcn_arch[64];       /* e.g. "gfx950:sramecc+:xnack-" */
+    int compute_units;
+    int clock_khz;           /* peak shader clock */
+    int memory_clock_khz;
+    int memory_bus_width;
+    size_t total_global_mem;
+    size_t lds_per_block;
+    int xcds;                /* best-effort; 8 on MI355X */
+} pyc_hip_device_info;
+
+/* Returns 0 and fills info for the current device, -1 when no HIP device. */
+int pyc_hip_device_query(pyc_hip_device_info* info);
+
+/* Number of kernel symbols compiled into this library for op_key
+ * ("matmul", "attention", "conv2d", "matmul_w8a16"), independent of the
+ * registry's state. */
+int pyc_hip_kernel_symbol_count(const char* op_key);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

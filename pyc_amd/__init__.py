@@ -1,0 +1,157 @@
+"""pyc_amd — MI355X (gfx950) backend for PyC's compiler-next run path.
+
+The product is the C-ABI shared library ``pyc_amd/lib/libpyc_amd.so`` (HIP
+kernels + C11 host engine, declared in ``include/pyc/*.h``). This package only
+loads it and offers thin Python wrappers that pass device pointers of torch
+tensors through that C-ABI; torch provides device memory and streams.
+
+Loading fails loudly: there is no Python or CPU fallback for any kernel.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+from . import abi
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libpyc_amd.so")
+
+_lib = None
+
+
+class PycError(RuntimeError):
+    pass
+
+
+def _declare(L: C.CDLL) -> None:
+    P, I, F, Z = C.c_void_p, C.c_int, C.c_float, C.c_size_t
+    S = C.c_char_p
+    L.pyc_hip_gemm_dispatch.argtypes = [S, I, I, I, P, P, P, F, F, P, I, P]
+    L.pyc_hip_gemm_dispatch.restype = I
+    L.pyc_cutlass_gemm_dispatch.argtypes = [S, I, I, I, P, P, P, F, F, P]
+    L.pyc_cutlass_gemm_dispatch.restype = I
+    L.pyc_hip_attention_dispatch.argtypes = [S, I, I, I, I, I, P, P, P, P, F, P]
+    L.pyc_hip_attention_dispatch.restype = I
+    L.pyc_cutlass_attention_dispatch.argtypes = [S, I, I, P, P, P, P, F, P]
+    L.pyc_cutlass_attention_dispatch.restype = I
+    L.pyc_hip_conv2d_dispatch.argtypes = [S] + [I] * 11 + [P, P, P, I, P, P]
+    L.pyc_hip_conv2d_dispatch.restype = I
+    L.pyc_cutlass_conv2d_dispatch.argtypes = [S] + [I] * 11 + [P, P, P, P]
+    L.pyc_cutlass_conv2d_dispatch.restype = I
+    L.pyc_hip_w8a16_gemm_dispatch.argtypes = [S, I, I, I, P, P, P, I, P, P]
+    L.pyc_hip_w8a16_gemm_dispatch.restype = I
+    L.pyc_hip_device_query.argtypes = [C.POINTER(abi.DeviceInfo)]
+    L.pyc_hip_device_query.restype = I
+    L.pyc_hip_kernel_symbol_count.argtypes = [S]
+    L.pyc_hip_kernel_symbol_count.restype = I
+    L.pyc_cutlass_kernel_count.argtypes = [S]
+    L.pyc_cutlass_kernel_count.restype = I
+    L.pyc_cutlass_registry_init.argtypes = []
+    L.pyc_cutlass_registry_init.restype = None
+    L.pyc_cuda_dispatch_trace_init.argtypes = [C.POINTER(abi.DispatchTrace)]
+    L.pyc_cuda_dispatch_trace_init.restype = None
+    L.pyc_cuda_current_hardware_family.argtypes = []
+    L.pyc_cuda_current_hardware_family.restype = I
+    L.pyc_cuda_dispatch.argtypes = [C.POINTER(abi.IrModule), C.POINTER(abi.Tensor), Z,
+                                    C.POINTER(abi.Tensor), Z, abi.CPU_EXECUTOR_FN, P,
+                                    C.POINTER(abi.DispatchTrace)]
+    L.pyc_cuda_dispatch.restype = I
+    # registry
+    L.pyc_kernel_registry_reset.argtypes = []
+    L.pyc_kernel_register.argtypes = [C.POINTER(abi.KernelDesc)]
+    L.pyc_kernel_register.restype = I
+    L.pyc_kernel_select.argtypes = [S, I, C.POINTER(abi.KernelDesc)]
+    L.pyc_kernel_select.restype = I
+    L.pyc_kernel_select_with_policy.argtypes = [S, I, I, C.c_double, C.POINTER(abi.KernelDesc),
+                                                C.POINTER(abi.KernelSelectionTrace)]
+    L.pyc_kernel_select_with_policy.restype = I
+    L.pyc_kernel_coselect_with_context.argtypes = [S, I, I, C.POINTER(abi.CoselectContext),
+                                                   C.POINTER(abi.KernelDesc),
+                                                   C.POINTER(abi.KernelSelectionTrace)]
+    L.pyc_kernel_coselect_with_context.restype = I
+    L.pyc_kernel_promote_symbol.argtypes = [S, I, S]
+    L.pyc_kernel_promote_symbol.restype = I
+    L.pyc_kernel_promoted_symbol.argtypes = [S, I, C.c_char_p, Z]
+    L.pyc_kernel_promoted_symbol.restype = I
+    L.pyc_kernel_benchmark_update_symbol.argtypes = [S, I, S, C.c_double]
+    L.pyc_kernel_benchmark_update_symbol.restype = I
+    L.pyc_kernel_benchmark_update.argtypes = [S, I, C.c_double]
+    L.pyc_kernel_benchmark_update.restype = I
+    L.pyc_kernel_benchmark_read.argtypes = [S, I, C.POINTER(abi.KernelBenchmark)]
+    L.pyc_kernel_benchmark_read.restype = None
+    L.pyc_kernel_collect.argtypes = [S, I, C.POINTER(abi.KernelDesc), Z]
+    L.pyc_kernel_collect.restype = Z
+    L.pyc_kernel_hardware_family_name.argtypes = [I]
+    L.pyc_kernel_hardware_family_name.restype = C.c_char_p
+    L.pyc_kernel_workload_family_name.argtypes = [I]
+    L.pyc_kernel_workload_family_name.restype = C.c_char_p
+
+
+def lib() -> C.CDLL:
+    """The loaded product library; raises PycError when it was not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise PycError(f"libpyc_amd.so is not built ({LIB_PATH}); run python -m pyc_amd.build")
+        L = C.CDLL(LIB_PATH)  # RTLD_LOCAL: never interposes other libraries
+        _declare(L)
+        _lib = L
+    return _lib
+
+
+def _b(s: str) -> bytes:
+    return s.encode()
+
+
+def _ptr(t) -> int:
+    return 0 if t is None else int(t.data_ptr())
+
+
+def _stream(stream) -> int:
+    if stream is not None:
+        return int(stream)
+    import torch
+    return int(torch.cuda.current_stream().cuda_stream)
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise PycError(f"{what} failed with status {rc}")
+
+
+def gemm(symbol: str, a, b, c, M: int, N: int, K: int, alpha: float = 1.0, beta: float = 0.0,
+         bias=None, epilogue: int = 0, stream=None) -> None:
+    """C = epi(alpha*A*op(B) + beta*C) through pyc_hip_gemm_dispatch (device tensors)."""
+    _check(lib().pyc_hip_gemm_dispatch(_b(symbol), M, N, K, _ptr(a), _ptr(b), _ptr(c), alpha, beta,
+                                       _ptr(bias), epilogue, _stream(stream)), f"gemm {symbol}")
+
+
+def attention(symbol: str, q, k, v, o, causal: bool, scale: float, stream=None) -> None:
+    B, H, S, D = q.shape
+    _check(lib().pyc_hip_attention_dispatch(_b(symbol), B, H, S, D, int(causal), _ptr(q), _ptr(k),
+                                            _ptr(v), _ptr(o), scale, _stream(stream)),
+           f"attention {symbol}")
+
+
+def conv2d(symbol: str, x, w, y, pad=(1, 1), stride=(1, 1), bias=None, relu: bool = False,
+           stream=None) -> None:
+    N, H, W, Cin = x.shape
+    K, R, S, _ = w.shape
+    _check(lib().pyc_hip_conv2d_dispatch(_b(symbol), N, H, W, Cin, K, R, S, pad[0], pad[1],
+                                         stride[0], stride[1], _ptr(x), _ptr(w), _ptr(bias),
+                                         int(relu), _ptr(y), _stream(stream)), f"conv2d {symbol}")
+
+
+def w8a16_gemm(x, wq, scale, y, relu: bool, stream=None,
+               symbol: str = "hip_gemm_w8a16_e4m3") -> None:
+    M, K = x.shape
+    N = wq.shape[0]
+    _check(lib().pyc_hip_w8a16_gemm_dispatch(_b(symbol), M, N, K, _ptr(x), _ptr(wq), _ptr(scale),
+                                             int(relu), _ptr(y), _stream(stream)), "w8a16 gemm")
+
+
+def device_info() -> abi.DeviceInfo:
+    info = abi.DeviceInfo()
+    _check(lib().pyc_hip_device_query(C.byref(info)), "device query")
+    return info

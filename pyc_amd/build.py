@@ -1,0 +1,87 @@
+"""Build recipe for libpyc_amd.so (gfx950 HIP kernels + C11 host engine).
+
+Usage: ``python -m pyc_amd.build`` (or ``__graft_entry__.build()``).
+
+* ``csrc/kernels/*.hip`` are compiled by hipcc for gfx950 only. Every HIP
+  compile carries ``-Xclang -target-feature -Xclang -packed-fp32-ops`` so the
+  compiler emits no packed-fp32 VALU instructions.
+* ``csrc/host/*.c`` are compiled as C11 by gcc against the HIP runtime C API.
+* Everything links into one in-tree shared library, ``pyc_amd/lib/libpyc_amd.so``,
+  whose exported C-ABI is declared in ``include/pyc/*.h``.
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import glob
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+HIPCC = os.path.join(ROCM, "bin", "hipcc")
+OBJ_DIR = os.path.join(HERE, "_build")
+LIB_DIR = os.path.join(HERE, "lib")
+LIB_PATH = os.path.join(LIB_DIR, "libpyc_amd.so")
+ARCH = "gfx950"
+
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-I", os.path.join(ROOT, "include"),
+]
+C_FLAGS = [
+    "-std=c11", "-O2", "-fPIC", "-Wall", "-Wno-unused-function",
+    "-Wno-stringop-truncation", "-Wno-format-truncation",
+    "-D_POSIX_C_SOURCE=200809L", "-D_DEFAULT_SOURCE", "-D__HIP_PLATFORM_AMD__",
+    "-I", os.path.join(ROOT, "include"), "-I", os.path.join(HERE, "csrc", "host"),
+    "-I", os.path.join(ROCM, "include"),
+]
+
+
+def _run(cmd: list[str]) -> None:
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in r.stdout.splitlines() if "packed-fp32-ops" not in l)
+    if r.returncode != 0:
+        raise RuntimeError(f"build step failed ({r.returncode}): {' '.join(cmd)}\n{out}")
+    if out.strip():
+        print(out, file=sys.stderr)
+
+
+def _obj(src: str) -> str:
+    base = os.path.relpath(src, os.path.join(HERE, "csrc")).replace(os.sep, "__")
+    return os.path.join(OBJ_DIR, base + ".o")
+
+
+def sources() -> tuple[list[str], list[str]]:
+    hip = sorted(glob.glob(os.path.join(HERE, "csrc", "kernels", "*.hip")))
+    c = sorted(glob.glob(os.path.join(HERE, "csrc", "host", "*.c")))
+    return hip, c
+
+
+def build(verbose: bool = True, jobs: int | None = None) -> str:
+    """Compile every source (always; this is the does-it-build check) and link."""
+    if not os.path.exists(HIPCC):
+        raise RuntimeError(f"hipcc not found at {HIPCC}")
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    os.makedirs(LIB_DIR, exist_ok=True)
+    hip, c = sources()
+    cmds = [[HIPCC, *HIP_FLAGS, "-c", s, "-o", _obj(s)] for s in hip]
+    cmds += [["gcc", *C_FLAGS, "-c", s, "-o", _obj(s)] for s in c]
+    jobs = jobs or min(8, os.cpu_count() or 4)
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        list(ex.map(_run, cmds))
+    tmp = LIB_PATH + ".tmp"
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp,
+          *[_obj(s) for s in hip + c], "-L", os.path.join(ROCM, "lib"), "-lamdhip64",
+          "-lpthread", "-lm", "-Wl,-Bsymbolic", f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}"])
+    shutil.move(tmp, LIB_PATH)
+    if verbose:
+        print(f"built {LIB_PATH} ({len(hip)} HIP + {len(c)} C sources)")
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    build()

@@ -1,0 +1,1313 @@
+/* hip_backend.c — MI355X GPU backend behind pyc_cuda_dispatch.
+ *
+ * Drop-in for reference src/compiler/runtime/cuda_backend.c. It keeps:
+ *   - the entry points and status codes of reference cuda_backend.h:28-98;
+ *   - the dispatch order and reason vocabulary of reference
+ *     cuda_backend.c:2808-2909 (forced_error, disabled_by_env,
+ *     cuda_simulated_available, cuda_runtime_detected / _no_device /
+ *     _error_%d, cuda_native_simulated, cuda_forced_fallback,
+ *     cuda_native_unsupported_fallback, cuda_native_failed_fallback,
+ *     <reason>;cpu_fallback_failed);
+ *   - the env contract (PYC_CUDA_DISABLE / FORCE_ERROR / FORCE_FALLBACK /
+ *     SIMULATE_AVAILABLE / ENABLE_GRAPH_REPLAY / ASSUME_STATIC_LHS|RHS /
+ *     SKIP_HOST_OUTPUT_COPY / BF16_GEMM_SYMBOL / ENABLE_PROMOTED_GEMM /
+ *     FORCE_HARDWARE_FAMILY); PYC_CUDA_ALLOW_TF32 / ENABLE_CUBLASLT /
+ *     LT_WORKSPACE_BYTES are accepted and ignored (no TF32, no BLAS library);
+ *   - one process-wide dispatch mutex (reference cuda_backend.c:13,2922-2926),
+ *     a grow-only device workspace released on any native failure (:413-549,
+ *     :2800-2803), static-operand upload skip (:2625-2636) and graph
+ *     capture/replay of [host->device copies, kernels, device->host copies]
+ *     keyed by a signature of the run (:1979-2253).
+ *
+ * What is new on MI355X: instead of pattern-matching one matmul[+add][+relu]
+ * and running the add/relu on the host after the copy back (reference
+ * cuda_backend.c:1232-1390, :1697-1742, :2783-2788), the module is lowered to a
+ * list of device steps - GEMM (fp32 / bf16 / fp16 MFMA, bias and ReLU fused
+ * into the epilogue), weight-only fp8 GEMM, NHWC conv (+bias +ReLU), causal
+ * attention - over device buffers, one per IR value. Chains of several
+ * matmuls therefore stay on the GPU and are captured into one hipGraph.
+ * Reasons of successful native runs keep the reference's prefixes:
+ *   hip_native_graph_capture / hip_native_graph_replay / hip_native
+ * plus ":<gemm symbol>" of the first GEMM step when there is one. */
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <time.h>
+
+#include <math.h>
+
+#include <hip/hip_runtime_api.h>
+
+#include "pyc/cuda_backend.h"
+#include "pyc/hip_backend.h"
+#include "pyc/kernel_registry.h"
+#include "pyc_mutex.h"
+
+static pyc_mutex g_dispatch_lock = PYC_MUTEX_INIT;
+
+/* ---------------------------------------------------------------- env */
+
+static int env_true(const char* name) {
+    const char* v = getenv(name);
+    return v && (strcmp(v, "1") == 0 || strcmp(v, "true") == 0 || strcmp(v, "TRUE") == 0);
+}
+
+static int env_default_true(const char* name) {
+    const char* v = getenv(name);
+    if (!v || v[0] == '\0') {
+        return 1;
+    }
+    return !(strcmp(v, "0") == 0 || strcmp(v, "false") == 0 || strcmp(v, "FALSE") == 0);
+}
+
+static double now_ms(void) {
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (double)ts.tv_sec * 1e3 + (double)ts.tv_nsec / 1e6;
+}
+
+static void set_reason(char* dst, size_t cap, const char* src) {
+    if (!dst || cap == 0) {
+        return;
+    }
+    strncpy(dst, src ? src : "", cap - 1);
+    dst[cap - 1] = '\0';
+}
+
+/* ---------------------------------------------------------------- trace / family */
+
+void pyc_cuda_dispatch_trace_init(pyc_cuda_dispatch_trace* trace) {
+    if (!trace) {
+        return;
+    }
+    memset(trace, 0, sizeof(*trace));
+    set_reason(trace->reason, sizeof(trace->reason), "not_requested");
+}
+
+static pyc_mutex g_family_lock = PYC_MUTEX_INIT;
+static int g_family_cached = 0;
+static pyc_kernel_hardware_family g_family = PYC_KERNEL_HARDWARE_GENERIC;
+
+pyc_kernel_hardware_family pyc_cuda_current_hardware_family(void) {
+    const char* force = getenv("PYC_CUDA_FORCE_HARDWARE_FAMILY");
+    pyc_kernel_hardware_family fam;
+    if (force && force[0] != '\0') {
+        if (strcmp(force, "cdna4") == 0 || strcmp(force, "mi355x") == 0) {
+            return PYC_KERNEL_HARDWARE_CDNA4;
+        }
+        if (strcmp(force, "hopper") == 0) {
+            return PYC_KERNEL_HARDWARE_HOPPER;
+        }
+        if (strcmp(force, "ada") == 0) {
+            return PYC_KERNEL_HARDWARE_ADA;
+        }
+        if (strcmp(force, "generic") == 0) {
+            return PYC_KERNEL_HARDWARE_GENERIC;
+        }
+    }
+    pyc_mutex_lock(&g_family_lock);
+    if (!g_family_cached) {
+        pyc_hip_device_info info;
+        g_family = PYC_KERNEL_HARDWARE_GENERIC;
+        if (pyc_hip_device_query(&info) == 0 && strncmp(info.gcn_arch, "gfx950", 6) == 0) {
+            g_family = PYC_KERNEL_HARDWARE_CDNA4;
+        }
+        g_family_cached = 1;
+    }
+    fam = g_family;
+    pyc_mutex_unlock(&g_family_lock);
+    return fam;
+}
+
+static int detect_gpu(char* reason, size_t cap) {
+    int count = 0;
+    hipError_t err;
+    if (env_true("PYC_CUDA_DISABLE")) {
+        set_reason(reason, cap, "disabled_by_env");
+        return 0;
+    }
+    if (env_true("PYC_CUDA_SIMULATE_AVAILABLE")) {
+        set_reason(reason, cap, "cuda_simulated_available");
+        return 1;
+    }
+    err = hipGetDeviceCount(&count);
+    if (err == hipSuccess && count > 0) {
+        set_reason(reason, cap, "cuda_runtime_detected");
+        return 1;
+    }
+    if (err != hipSuccess) {
+        snprintf(reason, cap, "cuda_runtime_error_%d", (int)err);
+    } else {
+        set_reason(reason, cap, "cuda_runtime_no_device");
+    }
+    return 0;
+}
+
+/* ---------------------------------------------------------------- lowering */
+
+static size_t dtype_bytes(pyc_dtype t) {
+    switch (t) {
+        case PYC_DTYPE_F32:
+        case PYC_DTYPE_I32:
+            return 4;
+        case PYC_DTYPE_F16:
+        case PYC_DTYPE_BF16:
+            return 2;
+        case PYC_DTYPE_I8:
+        case PYC_DTYPE_FP8_E4M3:
+            return 1;
+        default:
+            return 0;
+    }
+}
+
+static size_t shape_elems(const pyc_shape* s) {
+    size_t i, n = 1;
+    if (!s || s->rank == 0) {
+        return 0;
+    }
+    for (i = 0; i < s->rank; ++i) {
+        if (s->dims[i] <= 0) {
+            return 0;
+        }
+        n *= (size_t)s->dims[i];
+    }
+    return n;
+}
+
+enum { ST_GEMM = 1, ST_W8A16 = 2, ST_CONV = 3, ST_ATTN = 4 };
+enum { ADD_NONE = 0, ADD_MATRIX = 1, ADD_ROW_BIAS = 2, ADD_SCALAR = 3 };
+
+typedef struct {
+    int kind;
+    int out;      /* value id (op index) written */
+    int in[3];    /* value ids read */
+    int add_in;   /* value id of the fused add operand or -1 */
+    int add_mode;
+    int relu;
+    pyc_dtype dtype;
+    int m, n, k;  /* GEMM dims */
+    int conv[11]; /* N H W C K R S ph pw sh sw */
+    int attn[5];  /* B H S D causal */
+    char symbol[PYC_KERNEL_SYMBOL_MAX];
+} hip_step;
+
+typedef struct {
+    size_t nsteps;
+    hip_step steps[PYC_IR_MAX_OPS];
+    int value_op[PYC_IR_MAX_OPS];        /* op id -> op id holding its storage (fused ADD/RELU alias their producer) */
+    size_t value_bytes[PYC_IR_MAX_OPS];  /* bytes of each materialised value */
+    pyc_shape vshape[PYC_IR_MAX_OPS];    /* shape of each value (inferred for computed ones) */
+    pyc_dtype vdtype[PYC_IR_MAX_OPS];    /* element type of each value */
+    int input_ordinal[PYC_IR_MAX_OPS];   /* INPUT op -> inputs[] index, else -1 */
+    int output_src[64];
+    size_t n_outputs;
+    int is_weight[PYC_IR_MAX_OPS];       /* INPUT read as a GEMM rhs / conv filter / fp8 scale */
+    int f32_bias_needed[PYC_IR_MAX_OPS]; /* half add operand needing an fp32 device copy */
+} hip_plan;
+
+static int consumers(const pyc_ir_module* m, int id, int* only) {
+    size_t i, j;
+    int n = 0;
+    for (i = 0; i < m->op_count; ++i) {
+        for (j = 0; j < m->ops[i].input_count && j < PYC_IR_MAX_INPUTS; ++j) {
+            if (m->ops[i].input_ids[j] == id) {
+                n++;
+                if (only) {
+                    *only = (int)i;
+                }
+            }
+        }
+    }
+    return n;
+}
+
+static int valid_id(const pyc_ir_module* m, int id) {
+    return id >= 0 && (size_t)id < m->op_count;
+}
+
+/* conv attributes from the op name suffix "@s<sh>x<sw>p<ph>x<pw>" */
+static void conv_attrs(const char* name, int* sh, int* sw, int* ph, int* pw) {
+    const char* at = strchr(name, '@');
+    *sh = *sw = 1;
+    *ph = *pw = 0;
+    if (at) {
+        int a, b, c, d;
+        if (sscanf(at, "@s%dx%dp%dx%d", &a, &b, &c, &d) == 4) {
+            *sh = a;
+            *sw = b;
+            *ph = c;
+            *pw = d;
+        }
+    }
+}
+
+static void set_value(hip_plan* plan, int id, const pyc_shape* shape, pyc_dtype t) {
+    plan->vshape[id] = *shape;
+    plan->vdtype[id] = t;
+    plan->value_bytes[id] = shape_elems(shape) * dtype_bytes(t);
+}
+
+/* Absorb "x -> ADD(x, operand) -> RELU" after the GEMM/conv step `st` whose
+ * output value `prod` is viewed as [rows, cols]. Marks the absorbed ops in
+ * `covered` and makes them aliases of `prod`. */
+static void absorb_epilogue(const pyc_ir_module* m, int prod, size_t rows, size_t cols, hip_step* st,
+                            hip_plan* plan, int* covered) {
+    int next = -1;
+    int cur = prod;
+    st->add_in = -1;
+    st->add_mode = ADD_NONE;
+    st->relu = 0;
+    if (consumers(m, cur, &next) == 1 && m->ops[next].kind == PYC_IR_OP_ADD && m->ops[next].input_count >= 2) {
+        const pyc_ir_op* add = &m->ops[next];
+        int other = add->input_ids[0] == cur ? add->input_ids[1] : (add->input_ids[1] == cur ? add->input_ids[0] : -1);
+        if (valid_id(m, other) && m->ops[other].kind == PYC_IR_OP_INPUT) {
+            const pyc_shape* s = &m->ops[other].shape;
+            int mode = ADD_NONE;
+            if (s->rank == 2 && (size_t)s->dims[0] == rows && (size_t)s->dims[1] == cols) {
+                mode = ADD_MATRIX;
+            } else if (s->rank == 1 && (size_t)s->dims[0] == cols) {
+                mode = ADD_ROW_BIAS;
+            } else if (s->rank == 1 && s->dims[0] == 1) {
+                mode = ADD_SCALAR;
+            }
+            if (mode != ADD_NONE && (mode != ADD_MATRIX || m->ops[other].dtype == st->dtype) &&
+                (m->ops[other].dtype == PYC_DTYPE_F32 || m->ops[other].dtype == st->dtype)) {
+                st->add_in = other;
+                st->add_mode = mode;
+                if (mode != ADD_MATRIX && m->ops[other].dtype != PYC_DTYPE_F32) {
+                    plan->f32_bias_needed[other] = 1;
+                }
+                plan->value_op[next] = prod;
+                set_value(plan, next, &plan->vshape[prod], plan->vdtype[prod]);
+                covered[next] = 1;
+                cur = next;
+            }
+        }
+    }
+    next = -1;
+    if (consumers(m, cur, &next) == 1 && m->ops[next].kind == PYC_IR_OP_RELU) {
+        st->relu = 1;
+        plan->value_op[next] = prod;
+        set_value(plan, next, &plan->vshape[prod], plan->vdtype[prod]);
+        covered[next] = 1;
+    }
+}
+
+static const char* default_gemm_symbol(pyc_dtype t) {
+    if (t == PYC_DTYPE_BF16) {
+        const char* env = getenv("PYC_CUDA_BF16_GEMM_SYMBOL");
+        return (env && env[0] != '\0') ? env : "hip_gemm_bf16_nn";
+    }
+    if (t == PYC_DTYPE_F16) {
+        return "hip_gemm_f16_nn";
+    }
+    return "hip_gemm_f32_nn_64x64";
+}
+
+/* Build the device plan; returns 0 on success, 1 when some op has no native
+ * lowering (the caller then falls back). */
+static int build_plan(const pyc_ir_module* m, hip_plan* plan) {
+    size_t i;
+    int covered[PYC_IR_MAX_OPS];
+    size_t n_in = 0;
+    memset(covered, 0, sizeof(covered));
+    plan->nsteps = 0;
+    plan->n_outputs = 0;
+    for (i = 0; i < m->op_count; ++i) {
+        plan->value_op[i] = (int)i;
+        plan->value_bytes[i] = 0;
+        memset(&plan->vshape[i], 0, sizeof(pyc_shape));
+        plan->vdtype[i] = PYC_DTYPE_UNKNOWN;
+        plan->input_ordinal[i] = -1;
+        plan->is_weight[i] = 0;
+        plan->f32_bias_needed[i] = 0;
+    }
+    for (i = 0; i < m->op_count; ++i) {
+        const pyc_ir_op* op = &m->ops[i];
+        hip_step* st = &plan->steps[plan->nsteps];
+        if (covered[i]) {
+            continue;
+        }
+        switch (op->kind) {
+            case PYC_IR_OP_INPUT:
+                plan->input_ordinal[i] = (int)n_in++;
+                set_value(plan, (int)i, &op->shape, op->dtype);
+                if (plan->value_bytes[i] == 0) {
+                    return 1;
+                }
+                break;
+            case PYC_IR_OP_MATMUL: {
+                int a = op->input_count >= 2 ? op->input_ids[0] : -1;
+                int b = op->input_count >= 2 ? op->input_ids[1] : -1;
+                pyc_shape out_shape;
+                const pyc_shape *as, *bs;
+                if (!valid_id(m, a) || !valid_id(m, b) || a >= (int)i || b >= (int)i) {
+                    return 1;
+                }
+                a = plan->value_op[a];
+                b = plan->value_op[b];
+                as = &plan->vshape[a];
+                bs = &plan->vshape[b];
+                if (as->rank != 2 || bs->rank != 2) {
+                    return 1;
+                }
+                memset(st, 0, sizeof(*st));
+                st->out = (int)i;
+                st->in[0] = a;
+                st->in[1] = b;
+                st->in[2] = -1;
+                if (plan->vdtype[b] == PYC_DTYPE_FP8_E4M3) {
+                    /* weight-only fp8: rhs INPUT stored [N,K], third input = fp32 scale[N] */
+                    int sc = op->input_count >= 3 ? op->input_ids[2] : -1;
+                    if (!valid_id(m, sc) || m->ops[sc].kind != PYC_IR_OP_INPUT || m->ops[sc].dtype != PYC_DTYPE_F32 ||
+                        m->ops[b].kind != PYC_IR_OP_INPUT || plan->vdtype[a] != PYC_DTYPE_BF16) {
+                        return 1;
+                    }
+                    st->kind = ST_W8A16;
+                    st->dtype = PYC_DTYPE_BF16;
+                    st->m = (int)as->dims[0];
+                    st->k = (int)as->dims[1];
+                    st->n = (int)bs->dims[0];
+                    if (bs->dims[1] != st->k || m->ops[sc].shape.rank != 1 || m->ops[sc].shape.dims[0] != st->n ||
+                        st->m > 32 || (st->k % 16) != 0) {
+                        return 1;
+                    }
+                    st->in[2] = sc;
+                    plan->is_weight[b] = 1;
+                    plan->is_weight[sc] = 1;
+                    set_reason(st->symbol, sizeof(st->symbol), "hip_gemm_w8a16_e4m3");
+                } else {
+                    const pyc_dtype t = plan->vdtype[a];
+                    if (t != PYC_DTYPE_F32 && t != PYC_DTYPE_BF16 && t != PYC_DTYPE_F16) {
+                        return 1;
+                    }
+                    if (plan->vdtype[b] != t || (op->dtype != t && op->dtype != PYC_DTYPE_UNKNOWN)) {
+                        return 1;
+                    }
+                    st->kind = ST_GEMM;
+                    st->dtype = t;
+                    st->m = (int)as->dims[0];
+                    st->k = (int)as->dims[1];
+                    if (bs->dims[0] != st->k) {
+                        return 1;
+                    }
+                    st->n = (int)bs->dims[1];
+                    if (m->ops[b].kind == PYC_IR_OP_INPUT) {
+                        plan->is_weight[b] = 1;
+                    }
+                    set_reason(st->symbol, sizeof(st->symbol), default_gemm_symbol(t));
+                    if (t == PYC_DTYPE_F32 && env_true("PYC_CUDA_ENABLE_PROMOTED_GEMM")) {
+                        char promoted[PYC_KERNEL_SYMBOL_MAX];
+                        if (pyc_kernel_promoted_symbol("matmul", PYC_BACKEND_CUDA, promoted, sizeof(promoted)) == 0 &&
+                            (strcmp(promoted, "ada_gemm_k64_warp32_async_f32") == 0 ||
+                             strcmp(promoted, "hip_gemm_f32_nn_64x64") == 0)) {
+                            set_reason(st->symbol, sizeof(st->symbol), promoted);
+                        }
+                    }
+                }
+                memset(&out_shape, 0, sizeof(out_shape));
+                out_shape.rank = 2;
+                out_shape.dims[0] = st->m;
+                out_shape.dims[1] = st->n;
+                set_value(plan, (int)i, &out_shape, st->dtype);
+                absorb_epilogue(m, (int)i, (size_t)st->m, (size_t)st->n, st, plan, covered);
+                if (st->kind == ST_W8A16 && st->add_mode != ADD_NONE) {
+                    return 1; /* the fp8 epilogue is scale (+ReLU) only */
+                }
+                plan->nsteps++;
+                break;
+            }
+            case PYC_IR_OP_CONV2D: {
+                int x = op->input_count >= 2 ? op->input_ids[0] : -1;
+                int w = op->input_count >= 2 ? op->input_ids[1] : -1;
+                int sh, sw, ph, pw;
+                int64_t P, Q;
+                pyc_shape out_shape;
+                const pyc_shape *xs, *ws;
+                if (!valid_id(m, x) || !valid_id(m, w) || x >= (int)i || w >= (int)i) {
+                    return 1;
+                }
+                x = plan->value_op[x];
+                w = plan->value_op[w];
+                xs = &plan->vshape[x];
+                ws = &plan->vshape[w];
+                if (xs->rank != 4 || ws->rank != 4 || xs->dims[3] != ws->dims[3]) {
+                    return 1;
+                }
+                if ((plan->vdtype[x] != PYC_DTYPE_BF16 && plan->vdtype[x] != PYC_DTYPE_F16) ||
+                    plan->vdtype[w] != plan->vdtype[x]) {
+                    return 1;
+                }
+                conv_attrs(op->name, &sh, &sw, &ph, &pw);
+                memset(st, 0, sizeof(*st));
+                st->kind = ST_CONV;
+                st->dtype = plan->vdtype[x];
+                st->out = (int)i;
+                st->in[0] = x;
+                st->in[1] = w;
+                st->in[2] = -1;
+                st->conv[0] = (int)xs->dims[0];
+                st->conv[1] = (int)xs->dims[1];
+                st->conv[2] = (int)xs->dims[2];
+                st->conv[3] = (int)xs->dims[3];
+                st->conv[4] = (int)ws->dims[0];
+                st->conv[5] = (int)ws->dims[1];
+                st->conv[6] = (int)ws->dims[2];
+                st->conv[7] = ph;
+                st->conv[8] = pw;
+                st->conv[9] = sh;
+                st->conv[10] = sw;
+                if (sh <= 0 || sw <= 0 || ph < 0 || pw < 0 || st->conv[1] + 2 * ph < st->conv[5] ||
+                    st->conv[2] + 2 * pw < st->conv[6] || (st->conv[3] % 8) != 0) {
+                    return 1;
+                }
+                P = (st->conv[1] + 2 * ph - st->conv[5]) / sh + 1;
+                Q = (st->conv[2] + 2 * pw - st->conv[6]) / sw + 1;
+                if (m->ops[w].kind == PYC_IR_OP_INPUT) {
+                    plan->is_weight[w] = 1;
+                }
+                set_reason(st->symbol, sizeof(st->symbol),
+                           st->dtype == PYC_DTYPE_BF16 ? "hip_conv2d_bf16" : "hip_conv2d_f16");
+                memset(&out_shape, 0, sizeof(out_shape));
+                out_shape.rank = 4;
+                out_shape.dims[0] = st->conv[0];
+                out_shape.dims[1] = P;
+                out_shape.dims[2] = Q;
+                out_shape.dims[3] = st->conv[4];
+                set_value(plan, (int)i, &out_shape, st->dtype);
+                absorb_epilogue(m, (int)i, (size_t)(st->conv[0] * P * Q), (size_t)st->conv[4], st, plan, covered);
+                if (st->add_mode != ADD_NONE && st->add_mode != ADD_ROW_BIAS) {
+                    return 1;
+                }
+                plan->nsteps++;
+                break;
+            }
+            case PYC_IR_OP_ATTENTION: {
+                int q = op->input_count >= 3 ? op->input_ids[0] : -1;
+                int kk = op->input_count >= 3 ? op->input_ids[1] : -1;
+                int v = op->input_count >= 3 ? op->input_ids[2] : -1;
+                const pyc_shape* qs;
+                if (!valid_id(m, q) || !valid_id(m, kk) || !valid_id(m, v) || q >= (int)i || kk >= (int)i ||
+                    v >= (int)i) {
+                    return 1;
+                }
+                q = plan->value_op[q];
+                kk = plan->value_op[kk];
+                v = plan->value_op[v];
+                qs = &plan->vshape[q];
+                if (qs->rank != 4 || (plan->vdtype[q] != PYC_DTYPE_BF16 && plan->vdtype[q] != PYC_DTYPE_F16)) {
+                    return 1;
+                }
+                if (plan->vshape[kk].rank != 4 || plan->vshape[v].rank != 4 ||
+                    memcmp(plan->vshape[kk].dims, qs->dims, 4 * sizeof(int64_t)) != 0 ||
+                    memcmp(plan->vshape[v].dims, qs->dims, 4 * sizeof(int64_t)) != 0 ||
+                    plan->vdtype[kk] != plan->vdtype[q] || plan->vdtype[v] != plan->vdtype[q]) {
+                    return 1;
+                }
+                memset(st, 0, sizeof(*st));
+                st->kind = ST_ATTN;
+                st->dtype = plan->vdtype[q];
+                st->out = (int)i;
+                st->in[0] = q;
+                st->in[1] = kk;
+                st->in[2] = v;
+                st->add_in = -1;
+                st->attn[0] = (int)qs->dims[0];
+                st->attn[1] = (int)qs->dims[1];
+                st->attn[2] = (int)qs->dims[2];
+                st->attn[3] = (int)qs->dims[3];
+                st->attn[4] = strstr(op->name, "causal") != NULL;
+                if (st->attn[3] != 64 && st->attn[3] != 128) {
+                    return 1;
+                }
+                set_reason(st->symbol, sizeof(st->symbol),
+                           st->dtype == PYC_DTYPE_BF16 ? "hip_attention_bf16" : "hip_attention_f16");
+                set_value(plan, (int)i, qs, st->dtype);
+                plan->nsteps++;
+                break;
+            }
+            case PYC_IR_OP_OUTPUT: {
+                int src = op->input_count >= 1 ? op->input_ids[0] : -1;
+                if (!valid_id(m, src) || src >= (int)i || plan->n_outputs >= 64) {
+                    return 1;
+                }
+                src = plan->value_op[src];
+                if (plan->value_bytes[src] == 0) {
+                    return 1;
+                }
+                plan->output_src[plan->n_outputs++] = src;
+                break;
+            }
+            default:
+                return 1; /* ADD/RELU not absorbed, CONST, GELU, REDUCE_SUM, LAYERNORM */
+        }
+    }
+    return 0;
+}
+
+/* ---------------------------------------------------------------- workspace */
+
+typedef struct {
+    void* ptr;
+    size_t cap;
+} dbuf;
+
+typedef struct {
+    void* ptr;
+    size_t cap;
+} hbuf;
+
+static struct {
+    int ready;
+    int device;
+    hipStream_t stream;
+    hipEvent_t ev0, ev1;
+    dbuf val[PYC_IR_MAX_OPS];      /* device storage per value (op id) */
+    dbuf bias32[PYC_IR_MAX_OPS];   /* fp32 copies / fills of add operands */
+    hbuf stage_in[PYC_IR_MAX_OPS]; /* pinned staging per INPUT op */
+    hbuf stage_out[64];            /* pinned staging per output ordinal */
+    const void* last_host[PYC_IR_MAX_OPS];
+    size_t last_bytes[PYC_IR_MAX_OPS];
+    int uploaded[PYC_IR_MAX_OPS];
+    /* graph replay */
+    hipGraphExec_t gexec;
+    hipGraph_t graph;
+    int graph_valid;
+    uint64_t graph_sig;
+} g_ws;
+
+static void ws_release(void) {
+    size_t i;
+    if (g_ws.graph_valid) {
+        (void)hipGraphExecDestroy(g_ws.gexec);
+        (void)hipGraphDestroy(g_ws.graph);
+        g_ws.graph_valid = 0;
+    }
+    for (i = 0; i < PYC_IR_MAX_OPS; ++i) {
+        if (g_ws.val[i].ptr) {
+            (void)hipFree(g_ws.val[i].ptr);
+        }
+        if (g_ws.bias32[i].ptr) {
+            (void)hipFree(g_ws.bias32[i].ptr);
+        }
+        if (g_ws.stage_in[i].ptr) {
+            (void)hipHostFree(g_ws.stage_in[i].ptr);
+        }
+    }
+    for (i = 0; i < 64; ++i) {
+        if (g_ws.stage_out[i].ptr) {
+            (void)hipHostFree(g_ws.stage_out[i].ptr);
+        }
+    }
+    if (g_ws.ready) {
+        (void)hipEventDestroy(g_ws.ev0);
+        (void)hipEventDestroy(g_ws.ev1);
+        (void)hipStreamDestroy(g_ws.stream);
+    }
+    memset(&g_ws, 0, sizeof(g_ws));
+}
+
+static int ws_init(void) {
+    if (g_ws.ready) {
+        return 0;
+    }
+    memset(&g_ws, 0, sizeof(g_ws));
+    if (hipGetDevice(&g_ws.device) != hipSuccess) {
+        return -1;
+    }
+    if (hipStreamCreateWithFlags(&g_ws.stream, hipStreamNonBlocking) != hipSuccess) {
+        return -1;
+    }
+    if (hipEventCreate(&g_ws.ev0) != hipSuccess || hipEventCreate(&g_ws.ev1) != hipSuccess) {
+        return -1;
+    }
+    g_ws.ready = 1;
+    return 0;
+}
+
+/* Grow-only device buffer; growth invalidates a captured graph. */
+static int dgrow(dbuf* b, size_t bytes) {
+    if (b->cap >= bytes && b->ptr) {
+        return 0;
+    }
+    if (g_ws.graph_valid) {
+        (void)hipGraphExecDestroy(g_ws.gexec);
+        (void)hipGraphDestroy(g_ws.graph);
+        g_ws.graph_valid = 0;
+    }
+    if (b->ptr) {
+        (void)hipFree(b->ptr);
+        b->ptr = NULL;
+        b->cap = 0;
+    }
+    if (hipMalloc(&b->ptr, bytes) != hipSuccess) {
+        b->ptr = NULL;
+        return -1;
+    }
+    b->cap = bytes;
+    return 0;
+}
+
+static int hgrow(hbuf* b, size_t bytes) {
+    if (b->cap >= bytes && b->ptr) {
+        return 0;
+    }
+    if (g_ws.graph_valid) {
+        (void)hipGraphExecDestroy(g_ws.gexec);
+        (void)hipGraphDestroy(g_ws.graph);
+        g_ws.graph_valid = 0;
+    }
+    if (b->ptr) {
+        (void)hipHostFree(b->ptr);
+        b->ptr = NULL;
+        b->cap = 0;
+    }
+    if (hipHostMalloc(&b->ptr, bytes, hipHostMallocDefault) != hipSuccess) {
+        b->ptr = NULL;
+        return -1;
+    }
+    b->cap = bytes;
+    return 0;
+}
+
+static float bf16_bits_to_f32(uint16_t h) {
+    uint32_t u = ((uint32_t)h) << 16;
+    float f;
+    memcpy(&f, &u, sizeof(f));
+    return f;
+}
+
+static float f16_bits_to_f32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h >> 15) << 31;
+    int exp = (h >> 10) & 0x1f;
+    uint32_t man = h & 0x3ffu;
+    uint32_t u;
+    float f;
+    if (exp == 0x1f) {
+        u = sign | 0x7f800000u | (man << 13);
+    } else if (exp == 0) {
+        if (man == 0) {
+            u = sign;
+        } else {
+            exp = 1;
+            while (!(man & 0x400u)) {
+                man <<= 1;
+                exp--;
+            }
+            man &= 0x3ffu;
+            u = sign | ((uint32_t)(exp + 112) << 23) | (man << 13);
+        }
+    } else {
+        u = sign | ((uint32_t)(exp + 112) << 23) | (man << 13);
+    }
+    memcpy(&f, &u, sizeof(f));
+    return f;
+}
+
+/* ---------------------------------------------------------------- execution */
+
+static uint64_t fnv(uint64_t h, const void* p, size_t n) {
+    const unsigned char* c = (const unsigned char*)p;
+    size_t i;
+    for (i = 0; i < n; ++i) {
+        h ^= c[i];
+        h *= 1099511628211ull;
+    }
+    return h;
+}
+
+/* Enqueue the kernels of the plan on the workspace stream. */
+static int enqueue_steps(const pyc_ir_module* m, const hip_plan* plan, char* why, size_t why_cap) {
+    size_t s;
+    void* st_stream = (void*)g_ws.stream;
+    for (s = 0; s < plan->nsteps; ++s) {
+        const hip_step* st = &plan->steps[s];
+        void* out = g_ws.val[st->out].ptr;
+        int rc = -1;
+        int epi = (st->relu ? PYC_HIP_EPI_RELU : 0);
+        const float* bias = NULL;
+        float beta = 0.0f;
+        if (st->add_mode == ADD_ROW_BIAS || st->add_mode == ADD_SCALAR) {
+            epi |= PYC_HIP_EPI_BIAS;
+            /* an fp32 row bias is read where it was uploaded; scalar and half
+             * operands use their converted fp32 copy */
+            bias = (st->add_mode == ADD_ROW_BIAS && !plan->f32_bias_needed[st->add_in])
+                       ? (const float*)g_ws.val[st->add_in].ptr
+                       : (const float*)g_ws.bias32[st->add_in].ptr;
+        } else if (st->add_mode == ADD_MATRIX) {
+            /* C starts as the addend; beta = 1 folds it into the epilogue */
+            if (hipMemcpyAsync(out, g_ws.val[st->add_in].ptr, (size_t)st->m * st->n * dtype_bytes(st->dtype),
+                               hipMemcpyDeviceToDevice, g_ws.stream) != hipSuccess) {
+                snprintf(why, why_cap, "hip_copy_failed");
+                return -1;
+            }
+            beta = 1.0f;
+        }
+        switch (st->kind) {
+            case ST_GEMM:
+                rc = pyc_hip_gemm_dispatch(st->symbol, st->m, st->n, st->k, g_ws.val[st->in[0]].ptr,
+                                           g_ws.val[st->in[1]].ptr, out, 1.0f, beta, bias, epi, st_stream);
+                break;
+            case ST_W8A16:
+                rc = pyc_hip_w8a16_gemm_dispatch(st->symbol, st->m, st->n, st->k, g_ws.val[st->in[0]].ptr,
+                                                 g_ws.val[st->in[1]].ptr, (const float*)g_ws.val[st->in[2]].ptr,
+                                                 st->relu, out, st_stream);
+                break;
+            case ST_CONV:
+                rc = pyc_hip_conv2d_dispatch(st->symbol, st->conv[0], st->conv[1], st->conv[2], st->conv[3],
+                                             st->conv[4], st->conv[5], st->conv[6], st->conv[7], st->conv[8],
+                                             st->conv[9], st->conv[10], g_ws.val[st->in[0]].ptr,
+                                             g_ws.val[st->in[1]].ptr, bias, st->relu, out, st_stream);
+                break;
+            case ST_ATTN: {
+                const float scale = 1.0f / sqrtf((float)st->attn[3]);
+                rc = pyc_hip_attention_dispatch(st->symbol, st->attn[0], st->attn[1], st->attn[2], st->attn[3],
+                                                st->attn[4], g_ws.val[st->in[0]].ptr, g_ws.val[st->in[1]].ptr,
+                                                g_ws.val[st->in[2]].ptr, out, scale, st_stream);
+                break;
+            }
+            default:
+                break;
+        }
+        if (rc != 0) {
+            snprintf(why, why_cap, "hip_kernel_failed:%s", st->symbol);
+            return -1;
+        }
+    }
+    (void)m;
+    return 0;
+}
+
+static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size_t input_count,
+                          pyc_tensor* outputs, size_t output_count, pyc_cuda_dispatch_trace* trace,
+                          char* why, size_t why_cap) {
+    static hip_plan plan; /* guarded by g_dispatch_lock */
+    const int static_lhs = env_true("PYC_CUDA_ASSUME_STATIC_LHS");
+    const int static_rhs = env_true("PYC_CUDA_ASSUME_STATIC_RHS");
+    const int skip_out = env_true("PYC_CUDA_SKIP_HOST_OUTPUT_COPY");
+    const int use_graph = env_default_true("PYC_CUDA_ENABLE_GRAPH_REPLAY");
+    int copy_in[PYC_IR_MAX_OPS];
+    size_t i;
+    uint64_t sig = 1469598103934665603ull;
+    int replayed = 0;
+    double t0;
+    float dev_ms = 0.0f;
+
+    why[0] = '\0';
+    if (build_plan(m, &plan) != 0) {
+        return 1; /* unsupported pattern: not a failure of the GPU */
+    }
+    if (plan.n_outputs > output_count || plan.n_outputs > 64) {
+        return 1;
+    }
+    if (ws_init() != 0) {
+        snprintf(why, why_cap, "hip_workspace_init_failed");
+        return -1;
+    }
+
+    /* bind inputs, size checks, device + staging buffers */
+    for (i = 0; i < m->op_count; ++i) {
+        const int ord = plan.input_ordinal[i];
+        size_t bytes;
+        if (ord < 0) {
+            if (plan.value_bytes[i] && plan.value_op[i] == (int)i &&
+                dgrow(&g_ws.val[i], plan.value_bytes[i]) != 0) {
+                snprintf(why, why_cap, "hip_malloc_failed");
+                return -1;
+            }
+            continue;
+        }
+        if ((size_t)ord >= input_count || !inputs[ord].data) {
+            return 1;
+        }
+        bytes = plan.value_bytes[i];
+        if (inputs[ord].dtype != m->ops[i].dtype || inputs[ord].size_bytes < bytes) {
+            return 1;
+        }
+        if (dgrow(&g_ws.val[i], bytes) != 0 || hgrow(&g_ws.stage_in[i], bytes) != 0) {
+            snprintf(why, why_cap, "hip_malloc_failed");
+            return -1;
+        }
+        copy_in[i] = 1;
+        if (g_ws.uploaded[i] && g_ws.last_host[i] == inputs[ord].data && g_ws.last_bytes[i] == bytes &&
+            ((plan.is_weight[i] && static_rhs) || (!plan.is_weight[i] && static_lhs))) {
+            copy_in[i] = 0;
+        }
+    }
+    for (i = 0; i < plan.n_outputs; ++i) {
+        const int src = plan.output_src[i];
+        const size_t bytes = plan.value_bytes[src];
+        if (!skip_out && (!outputs[i].data || outputs[i].size_bytes < bytes)) {
+            return 1;
+        }
+        if (outputs[i].dtype != plan.vdtype[src]) {
+            return 1; /* output dtype must match the produced value */
+        }
+        if (hgrow(&g_ws.stage_out[i], bytes) != 0) {
+            snprintf(why, why_cap, "hip_malloc_failed");
+            return -1;
+        }
+    }
+    /* fp32 add operands: uploaded as part of the inputs; converted copies for half ones */
+    for (i = 0; i < plan.nsteps; ++i) {
+        const hip_step* st = &plan.steps[i];
+        if (st->add_in >= 0 && st->add_mode != ADD_MATRIX) {
+            const int ord = plan.input_ordinal[st->add_in];
+            const size_t cols = st->kind == ST_CONV ? (size_t)st->conv[4] : (size_t)st->n;
+            if (st->add_mode == ADD_ROW_BIAS && !plan.f32_bias_needed[st->add_in]) {
+                continue; /* fp32 row bias: used in place */
+            }
+            if (dgrow(&g_ws.bias32[st->add_in], cols * sizeof(float)) != 0) {
+                snprintf(why, why_cap, "hip_malloc_failed");
+                return -1;
+            }
+            if (ord < 0 || (size_t)ord >= input_count) {
+                return 1;
+            }
+            {
+                /* small host-side conversion / broadcast, then one upload */
+                float* tmp = (float*)malloc(cols * sizeof(float));
+                size_t c;
+                if (!tmp) {
+                    return -1;
+                }
+                for (c = 0; c < cols; ++c) {
+                    const size_t src_i = st->add_mode == ADD_SCALAR ? 0 : c;
+                    const pyc_dtype dt = m->ops[st->add_in].dtype;
+                    if (dt == PYC_DTYPE_F32) {
+                        tmp[c] = ((const float*)inputs[ord].data)[src_i];
+                    } else if (dt == PYC_DTYPE_BF16) {
+                        tmp[c] = bf16_bits_to_f32(((const uint16_t*)inputs[ord].data)[src_i]);
+                    } else {
+                        tmp[c] = f16_bits_to_f32(((const uint16_t*)inputs[ord].data)[src_i]);
+                    }
+                }
+                if (hipMemcpy(g_ws.bias32[st->add_in].ptr, tmp, cols * sizeof(float), hipMemcpyHostToDevice) != hipSuccess) {
+                    free(tmp);
+                    snprintf(why, why_cap, "hip_copy_failed");
+                    return -1;
+                }
+                free(tmp);
+            }
+        }
+    }
+
+    /* run signature: module content + host pointers + copy flags */
+    sig = fnv(sig, &m->op_count, sizeof(m->op_count));
+    sig = fnv(sig, m->ops, m->op_count * sizeof(pyc_ir_op));
+    sig = fnv(sig, &skip_out, sizeof(skip_out));
+    for (i = 0; i < m->op_count; ++i) {
+        if (plan.input_ordinal[i] >= 0) {
+            sig = fnv(sig, &copy_in[i], sizeof(int));
+        }
+    }
+
+    /* host -> pinned staging */
+    t0 = now_ms();
+    for (i = 0; i < m->op_count; ++i) {
+        const int ord = plan.input_ordinal[i];
+        if (ord >= 0 && copy_in[i]) {
+            memcpy(g_ws.stage_in[i].ptr, inputs[ord].data, plan.value_bytes[i]);
+        }
+    }
+    if (trace) {
+        trace->copy_in_ms += now_ms() - t0;
+    }
+
+    if (use_graph && g_ws.graph_valid && g_ws.graph_sig == sig) {
+        replayed = 1;
+    } else {
+        /* (re)record: either into a graph or directly */
+        hipError_t cerr = hipSuccess;
+        if (g_ws.graph_valid) {
+            (void)hipGraphExecDestroy(g_ws.gexec);
+            (void)hipGraphDestroy(g_ws.graph);
+            g_ws.graph_valid = 0;
+        }
+        if (use_graph) {
+            cerr = hipStreamBeginCapture(g_ws.stream, hipStreamCaptureModeThreadLocal);
+        }
+        if (cerr == hipSuccess) {
+            int rc = 0;
+            for (i = 0; i < m->op_count && rc == 0; ++i) {
+                if (plan.input_ordinal[i] >= 0 && copy_in[i]) {
+                    if (hipMemcpyAsync(g_ws.val[i].ptr, g_ws.stage_in[i].ptr, plan.value_bytes[i],
+                                       hipMemcpyHostToDevice, g_ws.stream) != hipSuccess) {
+                        rc = -1;
+                    }
+                }
+            }
+            if (rc == 0 && !use_graph) {
+                rc = hipEventRecord(g_ws.ev0, g_ws.stream) == hipSuccess ? 0 : -1;
+            }
+            if (rc == 0) {
+                rc = enqueue_steps(m, &plan, why, why_cap);
+            }
+            if (rc == 0 && !use_graph) {
+                rc = hipEventRecord(g_ws.ev1, g_ws.stream) == hipSuccess ? 0 : -1;
+            }
+            for (i = 0; rc == 0 && !skip_out && i < plan.n_outputs; ++i) {
+                const int src = plan.output_src[i];
+                if (hipMemcpyAsync(g_ws.stage_out[i].ptr, g_ws.val[src].ptr, plan.value_bytes[src],
+                                   hipMemcpyDeviceToHost, g_ws.stream) != hipSuccess) {
+                    rc = -1;
+                }
+            }
+            if (use_graph) {
+                hipGraph_t graph = NULL;
+                hipError_t e = hipStreamEndCapture(g_ws.stream, &graph);
+                if (rc == 0 && e == hipSuccess && graph &&
+                    hipGraphInstantiate(&g_ws.gexec, graph, NULL, NULL, 0) == hipSuccess) {
+                    g_ws.graph = graph;
+                    g_ws.graph_valid = 1;
+                    g_ws.graph_sig = sig;
+                } else {
+                    if (graph) {
+                        (void)hipGraphDestroy(graph);
+                    }
+                    if (why[0] == '\0') {
+                        snprintf(why, why_cap, "hip_graph_capture_failed");
+                    }
+                    return -1;
+                }
+            } else if (rc != 0) {
+                if (why[0] == '\0') {
+                    snprintf(why, why_cap, "hip_enqueue_failed");
+                }
+                return -1;
+            }
+        } else {
+            snprintf(why, why_cap, "hip_graph_begin_failed");
+            return -1;
+        }
+    }
+
+    t0 = now_ms();
+    if (use_graph) {
+        if (hipEventRecord(g_ws.ev0, g_ws.stream) != hipSuccess ||
+            hipGraphLaunch(g_ws.gexec, g_ws.stream) != hipSuccess ||
+            hipEventRecord(g_ws.ev1, g_ws.stream) != hipSuccess) {
+            snprintf(why, why_cap, "hip_graph_launch_failed");
+            return -1;
+        }
+    }
+    if (hipStreamSynchronize(g_ws.stream) != hipSuccess) {
+        snprintf(why, why_cap, "hip_sync_failed");
+        return -1;
+    }
+    if (trace) {
+        trace->sync_ms += now_ms() - t0;
+        if (hipEventElapsedTime(&dev_ms, g_ws.ev0, g_ws.ev1) == hipSuccess) {
+            trace->kernel_ms += (double)dev_ms;
+        }
+        trace->graph_replayed = replayed;
+    }
+
+    /* pinned staging -> caller buffers */
+    t0 = now_ms();
+    for (i = 0; !skip_out && i < plan.n_outputs; ++i) {
+        memcpy(outputs[i].data, g_ws.stage_out[i].ptr, plan.value_bytes[plan.output_src[i]]);
+    }
+    if (trace) {
+        trace->copy_out_ms += now_ms() - t0;
+    }
+    for (i = 0; i < m->op_count; ++i) {
+        const int ord = plan.input_ordinal[i];
+        if (ord >= 0 && copy_in[i]) {
+            g_ws.uploaded[i] = 1;
+            g_ws.last_host[i] = inputs[ord].data;
+            g_ws.last_bytes[i] = plan.value_bytes[i];
+        }
+    }
+
+    {
+        const char* base = replayed ? "hip_native_graph_replay" : (use_graph ? "hip_native_graph_capture" : "hip_native");
+        const char* sym = NULL;
+        for (i = 0; i < plan.nsteps; ++i) {
+            if (plan.steps[i].kind == ST_GEMM || plan.steps[i].kind == ST_W8A16) {
+                sym = plan.steps[i].symbol;
+                break;
+            }
+        }
+        if (!sym && plan.nsteps > 0) {
+            sym = plan.steps[0].symbol;
+        }
+        if (sym) {
+            snprintf(why, why_cap, "%s:%s", base, sym);
+        } else {
+            set_reason(why, why_cap, base);
+        }
+    }
+    return 0;
+}
+
+/* ---------------------------------------------------------------- simulated executor */
+
+/* PYC_CUDA_SIMULATE_AVAILABLE: a host-only stand-in for the GPU that lets the
+ * dispatch contract be exercised without a device (reference
+ * cuda_backend.c:1413-1671): naive fp32 matmul, broadcast add, relu, and
+ * byte-exact passthrough of any dtype. It never runs unless that variable is
+ * set, and its runs are reported as "cuda_native_simulated". */
+static int execute_simulated(const pyc_ir_module* m, const pyc_tensor* inputs, size_t input_count,
+                             pyc_tensor* outputs, size_t output_count) {
+    const void* val[PYC_IR_MAX_OPS];
+    void* owned[PYC_IR_MAX_OPS];
+    size_t bytes[PYC_IR_MAX_OPS];
+    size_t i, nin = 0, nout = 0;
+    int fail = 0;
+    memset(owned, 0, sizeof(owned));
+    memset(val, 0, sizeof(val));
+    for (i = 0; i < m->op_count && !fail; ++i) {
+        const pyc_ir_op* op = &m->ops[i];
+        const size_t elems = shape_elems(&op->shape);
+        switch (op->kind) {
+            case PYC_IR_OP_INPUT:
+                if (nin >= input_count || !inputs[nin].data || inputs[nin].dtype != op->dtype ||
+                    inputs[nin].size_bytes < elems * dtype_bytes(op->dtype) || elems == 0) {
+                    fail = 1;
+                    break;
+                }
+                val[i] = inputs[nin].data;
+                bytes[i] = elems * dtype_bytes(op->dtype);
+                nin++;
+                break;
+            case PYC_IR_OP_MATMUL: {
+                const int a = op->input_ids[0], b = op->input_ids[1];
+                size_t M, K, N, r, c, t;
+                float* out;
+                if (op->input_count < 2 || !valid_id(m, a) || !valid_id(m, b) || !val[a] || !val[b] ||
+                    op->dtype != PYC_DTYPE_F32 || m->ops[a].shape.rank != 2 || m->ops[b].shape.rank != 2 ||
+                    m->ops[a].shape.dims[1] != m->ops[b].shape.dims[0]) {
+                    fail = 1;
+                    break;
+                }
+                M = (size_t)m->ops[a].shape.dims[0];
+                K = (size_t)m->ops[a].shape.dims[1];
+                N = (size_t)m->ops[b].shape.dims[1];
+                out = (float*)malloc(M * N * sizeof(float));
+                if (!out) {
+                    fail = 1;
+                    break;
+                }
+                for (r = 0; r < M; ++r) {
+                    for (c = 0; c < N; ++c) {
+                        float acc = 0.0f;
+                        for (t = 0; t < K; ++t) {
+                            acc += ((const float*)val[a])[r * K + t] * ((const float*)val[b])[t * N + c];
+                        }
+                        out[r * N + c] = acc;
+                    }
+                }
+                owned[i] = out;
+                val[i] = out;
+                bytes[i] = M * N * sizeof(float);
+                break;
+            }
+            case PYC_IR_OP_ADD: {
+                const int a = op->input_ids[0], b = op->input_ids[1];
+                size_t na, nb, j;
+                float* out;
+                if (op->input_count < 2 || !valid_id(m, a) || !valid_id(m, b) || !val[a] || !val[b] ||
+                    op->dtype != PYC_DTYPE_F32) {
+                    fail = 1;
+                    break;
+                }
+                na = bytes[a] / sizeof(float);
+                nb = bytes[b] / sizeof(float);
+                if (nb > na) {
+                    const int tmp = a;
+                    (void)tmp;
+                    fail = 1;
+                    break;
+                }
+                out = (float*)malloc(na * sizeof(float));
+                if (!out || nb == 0 || na % nb != 0) {
+                    free(out);
+                    fail = 1;
+                    break;
+                }
+                for (j = 0; j < na; ++j) {
+                    out[j] = ((const float*)val[a])[j] + ((const float*)val[b])[j % nb];
+                }
+                owned[i] = out;
+                val[i] = out;
+                bytes[i] = na * sizeof(float);
+                break;
+            }
+            case PYC_IR_OP_RELU: {
+                const int a = op->input_ids[0];
+                size_t n, j;
+                float* out;
+                if (op->input_count < 1 || !valid_id(m, a) || !val[a] || op->dtype != PYC_DTYPE_F32) {
+                    fail = 1;
+                    break;
+                }
+                n = bytes[a] / sizeof(float);
+                out = (float*)malloc(n * sizeof(float));
+                if (!out) {
+                    fail = 1;
+                    break;
+                }
+                for (j = 0; j < n; ++j) {
+                    const float v = ((const float*)val[a])[j];
+                    out[j] = v > 0.0f ? v : 0.0f;
+                }
+                owned[i] = out;
+                val[i] = out;
+                bytes[i] = n * sizeof(float);
+                break;
+            }
+            case PYC_IR_OP_OUTPUT: {
+                const int a = op->input_ids[0];
+                if (op->input_count < 1 || !valid_id(m, a) || !val[a] || nout >= output_count ||
+                    !outputs[nout].data || outputs[nout].size_bytes < bytes[a]) {
+                    fail = 1;
+                    break;
+                }
+                memcpy(outputs[nout].data, val[a], bytes[a]);
+                nout++;
+                break;
+            }
+            default:
+                fail = 1;
+                break;
+        }
+    }
+    for (i = 0; i < m->op_count; ++i) {
+        free(owned[i]);
+    }
+    return fail ? -1 : 0;
+}
+
+/* ---------------------------------------------------------------- dispatch */
+
+static int native_kind_supported(const pyc_ir_module* m) {
+    size_t i;
+    if (!m || m->op_count == 0) {
+        return 0;
+    }
+    for (i = 0; i < m->op_count; ++i) {
+        switch (m->ops[i].kind) {
+            case PYC_IR_OP_INPUT:
+            case PYC_IR_OP_MATMUL:
+            case PYC_IR_OP_ADD:
+            case PYC_IR_OP_RELU:
+            case PYC_IR_OP_OUTPUT:
+            case PYC_IR_OP_CONV2D:
+            case PYC_IR_OP_ATTENTION:
+                break;
+            default:
+                return 0;
+        }
+        if (dtype_bytes(m->ops[i].dtype) == 0 && m->ops[i].kind != PYC_IR_OP_OUTPUT) {
+            return 0;
+        }
+    }
+    return 1;
+}
+
+static pyc_cuda_dispatch_status dispatch_locked(const pyc_ir_module* module, const pyc_tensor* inputs,
+                                                size_t input_count, pyc_tensor* outputs, size_t output_count,
+                                                pyc_cpu_executor_fn cpu_executor, void* executor_ctx,
+                                                pyc_cuda_dispatch_trace* trace) {
+    char reason[PYC_CUDA_REASON_MAX];
+    char native[PYC_CUDA_REASON_MAX];
+    int available;
+    int supported;
+    int native_rc = 1;
+
+    if (!module || !inputs || !outputs || !cpu_executor) {
+        return PYC_CUDA_DISPATCH_ERROR;
+    }
+    pyc_cuda_dispatch_trace_init(trace);
+    if (trace) {
+        trace->cuda_requested = 1;
+    }
+    if (env_true("PYC_CUDA_FORCE_ERROR")) {
+        if (trace) {
+            trace->cuda_available = 0;
+            trace->fallback_to_cpu = 0;
+            set_reason(trace->reason, sizeof(trace->reason), "forced_error");
+        }
+        return PYC_CUDA_DISPATCH_ERROR;
+    }
+    reason[0] = '\0';
+    native[0] = '\0';
+    available = detect_gpu(reason, sizeof(reason));
+    if (trace) {
+        trace->cuda_available = available;
+    }
+    supported = native_kind_supported(module);
+    if (available && supported && !env_true("PYC_CUDA_FORCE_FALLBACK")) {
+        int count = 0;
+        /* a real device is tried first, also when the simulation flag is set
+         * (reference cuda_backend.c:2856-2880) */
+        if (hipGetDeviceCount(&count) == hipSuccess && count > 0) {
+            native_rc = execute_native(module, inputs, input_count, outputs, output_count, trace, native,
+                                       sizeof(native));
+            if (native_rc == 0) {
+                if (trace) {
+                    trace->fallback_to_cpu = 0;
+                    set_reason(trace->reason, sizeof(trace->reason), native);
+                }
+                return PYC_CUDA_DISPATCH_OK;
+            }
+            if (native_rc < 0) {
+                ws_release();
+            }
+        }
+        if (env_true("PYC_CUDA_SIMULATE_AVAILABLE") &&
+            execute_simulated(module, inputs, input_count, outputs, output_count) == 0) {
+            if (trace) {
+                trace->fallback_to_cpu = 0;
+                set_reason(trace->reason, sizeof(trace->reason), "cuda_native_simulated");
+            }
+            return PYC_CUDA_DISPATCH_OK;
+        }
+    }
+
+    if (cpu_executor(module, inputs, input_count, outputs, output_count, executor_ctx) != 0) {
+        if (trace) {
+            trace->fallback_to_cpu = 0;
+            if (native[0] != '\0') {
+                snprintf(trace->reason, sizeof(trace->reason), "%.100s;cpu_fallback_failed", native);
+            } else {
+                set_reason(trace->reason, sizeof(trace->reason), "cpu_fallback_failed");
+            }
+        }
+        return PYC_CUDA_DISPATCH_ERROR;
+    }
+    if (trace) {
+        trace->fallback_to_cpu = 1;
+        if (env_true("PYC_CUDA_FORCE_FALLBACK")) {
+            set_reason(trace->reason, sizeof(trace->reason), "cuda_forced_fallback");
+        } else if (available && (!supported || native_rc > 0)) {
+            set_reason(trace->reason, sizeof(trace->reason), "cuda_native_unsupported_fallback");
+        } else if (available) {
+            set_reason(trace->reason, sizeof(trace->reason), "cuda_native_failed_fallback");
+        } else {
+            set_reason(trace->reason, sizeof(trace->reason), reason);
+        }
+    }
+    return PYC_CUDA_DISPATCH_FALLBACK;
+}
+
+pyc_cuda_dispatch_status pyc_cuda_dispatch(const pyc_ir_module* module, const pyc_tensor* inputs,
+                                           size_t input_count, pyc_tensor* outputs, size_t output_count,
+                                           pyc_cpu_executor_fn cpu_executor, void* executor_ctx,
+                                           pyc_cuda_dispatch_trace* trace) {
+    pyc_cuda_dispatch_status st;
+    pyc_mutex_lock(&g_dispatch_lock);
+    st = dispatch_locked(module, inputs, input_count, outputs, output_count, cpu_executor, executor_ctx, trace);
+    pyc_mutex_unlock(&g_dispatch_lock);
+    return st;
+}
+
+/* Releases every device/pinned buffer, the stream and the captured graph. */
+void pyc_hip_backend_release(void) {
+    pyc_mutex_lock(&g_dispatch_lock);
+    ws_release();
+    pyc_mutex_unlock(&g_dispatch_lock);
+}

@@ -1,0 +1,290 @@
+/* hip_kernels.c — kernel-level C-ABI of the MI355X backend.
+ *
+ * Implements the symbol-dispatched entry points the reference exposes for its
+ * CUTLASS kernels (reference include/pyc/cuda_backend.h:105-143,
+ * src/compiler/cutlass_kernels/{gemm,conv2d,attention,registry}/*.cu) and the
+ * MI355X extensions declared in pyc/hip_backend.h. Every symbol resolves to a
+ * hand-written gfx950 kernel through the variant table below; there is no
+ * library GEMM and no CPU path behind these functions.
+ *
+ * Argument checks happen here on the host, before any launch, so a kernel is
+ * never started on a shape its grid does not cover. */
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <hip/hip_runtime_api.h>
+
+#include "pyc/cuda_backend.h"
+#include "pyc/hip_backend.h"
+#include "pyc/kernel_registry.h"
+#include "pyc_mutex.h"
+
+/* ---------------------------------------------------------------- launchers (.hip) */
+int pyc_hip_gemm_half_launch(int is_bf16, int b_trans, int tile, int M, int N, int K,
+                             const void* A, const void* B, void* C, float alpha, float beta,
+                             const float* bias, int epi, void* stream);
+int pyc_hip_gemm_f32_launch(int b_trans, int M, int N, int K, const void* A, const void* B,
+                            void* C, float alpha, float beta, const float* bias, int epi,
+                            void* stream);
+int pyc_hip_attention_launch(int is_bf16, int B, int H, int S, int D, int causal, const void* Q,
+                             const void* K, const void* V, void* O, float scale, void* stream);
+int pyc_hip_conv2d_launch(int is_bf16, int N, int H, int W, int C, int K, int R, int S, int ph,
+                          int pw, int sh, int sw, const void* x, const void* w, const float* bias,
+                          int relu, void* y, void* stream);
+int pyc_hip_w8a16_launch(int M, int N, int K, const void* X, const void* Wq, const float* scale,
+                         int relu, void* Y, void* stream);
+
+/* ---------------------------------------------------------------- variant table */
+
+enum { VK_GEMM = 1, VK_ATTN = 2, VK_CONV = 3, VK_W8 = 4 };
+enum { VT_BF16 = 1, VT_F16 = 2, VT_F32 = 3 };
+
+typedef struct {
+    const char* op_key;
+    const char* symbol;
+    int kind;
+    int dtype;
+    int b_trans;  /* GEMM: B stored [N,K] */
+    int tile;     /* GEMM half tile edge; 0 = choose by shape */
+    int unit_epilogue_only; /* alpha must be 1 and beta 0 */
+    int priority;
+    double occupancy;      /* waves per SIMD / 8 for the variant's launch bounds */
+    size_t lds_bytes;
+    int reg_class;
+    pyc_kernel_workload_family workload;
+} hip_variant;
+
+static const hip_variant k_variants[] = {
+    /* bf16 MFMA GEMM tiles */
+    {"matmul", "hip_gemm_bf16_nt_256x256", VK_GEMM, VT_BF16, 1, 256, 0, 120, 0.125, 131072, 3, PYC_KERNEL_WORKLOAD_LARGE_SQUARE},
+    {"matmul", "hip_gemm_bf16_nt_128x128", VK_GEMM, VT_BF16, 1, 128, 0, 110, 0.25, 65536, 2, PYC_KERNEL_WORKLOAD_SQUARE},
+    {"matmul", "hip_gemm_bf16_nn_256x256", VK_GEMM, VT_BF16, 0, 256, 0, 115, 0.125, 131072, 3, PYC_KERNEL_WORKLOAD_LARGE_SQUARE},
+    {"matmul", "hip_gemm_bf16_nn_128x128", VK_GEMM, VT_BF16, 0, 128, 0, 105, 0.25, 65536, 2, PYC_KERNEL_WORKLOAD_SQUARE},
+    {"matmul", "hip_gemm_bf16_nt", VK_GEMM, VT_BF16, 1, 0, 0, 100, 0.125, 131072, 3, PYC_KERNEL_WORKLOAD_ANY},
+    {"matmul", "hip_gemm_bf16_nn", VK_GEMM, VT_BF16, 0, 0, 0, 100, 0.125, 131072, 3, PYC_KERNEL_WORKLOAD_ANY},
+    /* fp16 MFMA GEMM */
+    {"matmul", "hip_gemm_f16_nt", VK_GEMM, VT_F16, 1, 0, 0, 95, 0.125, 131072, 3, PYC_KERNEL_WORKLOAD_ANY},
+    {"matmul", "hip_gemm_f16_nn", VK_GEMM, VT_F16, 0, 0, 0, 95, 0.125, 131072, 3, PYC_KERNEL_WORKLOAD_ANY},
+    /* fp32 MFMA GEMM (true fp32) */
+    {"matmul", "hip_gemm_f32_nn_64x64", VK_GEMM, VT_F32, 0, 64, 0, 60, 0.25, 32768, 1, PYC_KERNEL_WORKLOAD_ANY},
+    {"matmul", "hip_gemm_f32_nt_64x64", VK_GEMM, VT_F32, 1, 64, 0, 55, 0.25, 32768, 1, PYC_KERNEL_WORKLOAD_ANY},
+    /* reference symbol names (reference gemm/kernel.cu:105-145, ada_async_kernel.cu:252-266),
+     * bound to the MI355X kernels with the reference's operand layouts */
+    {"matmul", "cutlass_gemm_tensorcore_f16", VK_GEMM, VT_F16, 1, 0, 0, 100, 0.125, 131072, 2, PYC_KERNEL_WORKLOAD_ANY},
+    {"matmul", "cutlass_gemm_tensorcore_bf16", VK_GEMM, VT_BF16, 0, 0, 0, 90, 0.125, 131072, 2, PYC_KERNEL_WORKLOAD_ANY},
+    {"matmul", "cutlass_gemm_simt_f32", VK_GEMM, VT_F32, 1, 64, 0, 10, 0.25, 32768, 1, PYC_KERNEL_WORKLOAD_ANY},
+    {"matmul", "ada_gemm_k64_warp32_async_f32", VK_GEMM, VT_F32, 0, 64, 1, 20, 0.25, 32768, 1, PYC_KERNEL_WORKLOAD_ANY},
+    /* attention (reference attention/kernel.cu:64-90 names) */
+    {"attention", "hip_attention_bf16", VK_ATTN, VT_BF16, 0, 0, 0, 110, 0.25, 49152, 3, PYC_KERNEL_WORKLOAD_ANY},
+    {"attention", "hip_attention_f16", VK_ATTN, VT_F16, 0, 0, 0, 105, 0.25, 49152, 3, PYC_KERNEL_WORKLOAD_ANY},
+    {"attention", "cutlass_attention_f16", VK_ATTN, VT_F16, 0, 0, 0, 100, 0.25, 49152, 3, PYC_KERNEL_WORKLOAD_ANY},
+    {"attention", "cutlass_attention_bf16", VK_ATTN, VT_BF16, 0, 0, 0, 90, 0.25, 49152, 3, PYC_KERNEL_WORKLOAD_ANY},
+    /* conv2d (reference conv2d/kernel.cu:48-75 names) */
+    {"conv2d", "hip_conv2d_bf16", VK_CONV, VT_BF16, 0, 0, 0, 110, 0.125, 131072, 3, PYC_KERNEL_WORKLOAD_ANY},
+    {"conv2d", "hip_conv2d_f16", VK_CONV, VT_F16, 0, 0, 0, 105, 0.125, 131072, 3, PYC_KERNEL_WORKLOAD_ANY},
+    {"conv2d", "cutlass_conv2d_fprop_f16", VK_CONV, VT_F16, 0, 0, 0, 100, 0.125, 131072, 2, PYC_KERNEL_WORKLOAD_ANY},
+    {"conv2d", "cutlass_conv2d_fprop_bf16", VK_CONV, VT_BF16, 0, 0, 0, 90, 0.125, 131072, 2, PYC_KERNEL_WORKLOAD_ANY},
+    /* weight-only fp8 decode GEMM (no reference counterpart) */
+    {"matmul_w8a16", "hip_gemm_w8a16_e4m3", VK_W8, VT_BF16, 1, 0, 0, 100, 0.5, 16384, 2, PYC_KERNEL_WORKLOAD_WIDE_SKINNY},
+};
+
+static const hip_variant* find_variant(const char* symbol, int kind) {
+    size_t i;
+    if (!symbol) {
+        return NULL;
+    }
+    for (i = 0; i < sizeof(k_variants) / sizeof(k_variants[0]); ++i) {
+        if (k_variants[i].kind == kind && strcmp(k_variants[i].symbol, symbol) == 0) {
+            return &k_variants[i];
+        }
+    }
+    return NULL;
+}
+
+int pyc_hip_kernel_symbol_count(const char* op_key) {
+    size_t i;
+    int n = 0;
+    if (!op_key) {
+        return 0;
+    }
+    for (i = 0; i < sizeof(k_variants) / sizeof(k_variants[0]); ++i) {
+        n += strcmp(k_variants[i].op_key, op_key) == 0;
+    }
+    return n;
+}
+
+/* ---------------------------------------------------------------- GEMM */
+
+/* Tile choice for shape-generic symbols: the 256x256 tile when it still gives
+ * at least one workgroup per CU (256 CUs on MI355X), else 128x128. */
+static int pick_half_tile(int M, int N) {
+    const long t256 = (long)((M + 255) / 256) * (long)((N + 255) / 256);
+    return t256 >= 256 ? 256 : 128;
+}
+
+static int gemm_run(const hip_variant* v, int M, int N, int K, const void* A, const void* B,
+                    void* C, float alpha, float beta, const float* bias, int epilogue, void* stream) {
+    if (!v || M <= 0 || N <= 0 || K <= 0 || !A || !B || !C) {
+        return -1;
+    }
+    if ((epilogue & PYC_HIP_EPI_BIAS) && !bias) {
+        return -1;
+    }
+    if (v->unit_epilogue_only && (alpha != 1.0f || beta != 0.0f)) {
+        return -1;
+    }
+    if (v->dtype == VT_F32) {
+        return pyc_hip_gemm_f32_launch(v->b_trans, M, N, K, A, B, C, alpha, beta, bias, epilogue, stream);
+    }
+    return pyc_hip_gemm_half_launch(v->dtype == VT_BF16, v->b_trans, v->tile ? v->tile : pick_half_tile(M, N),
+                                    M, N, K, A, B, C, alpha, beta, bias, epilogue, stream);
+}
+
+int pyc_hip_gemm_dispatch(const char* symbol, int M, int N, int K, const void* A, const void* B,
+                          void* C, float alpha, float beta, const float* bias, int epilogue,
+                          void* stream) {
+    return gemm_run(find_variant(symbol, VK_GEMM), M, N, K, A, B, C, alpha, beta, bias, epilogue, stream);
+}
+
+int pyc_cutlass_gemm_dispatch(const char* symbol, int M, int N, int K, const void* A, const void* B,
+                              void* C, float alpha, float beta, void* stream) {
+    const int rc = gemm_run(find_variant(symbol, VK_GEMM), M, N, K, A, B, C, alpha, beta, NULL,
+                            PYC_HIP_EPI_NONE, stream);
+    return rc == 0 ? 0 : -1;
+}
+
+/* ---------------------------------------------------------------- attention */
+
+int pyc_hip_attention_dispatch(const char* symbol, int B, int H, int S, int D, int causal,
+                               const void* Q, const void* K, const void* V, void* O, float scale,
+                               void* stream) {
+    const hip_variant* v = find_variant(symbol, VK_ATTN);
+    if (!v || B <= 0 || H <= 0 || S <= 0 || !Q || !K || !V || !O) {
+        return -1;
+    }
+    if (D != 64 && D != 128) {
+        return -1;
+    }
+    return pyc_hip_attention_launch(v->dtype == VT_BF16, B, H, S, D, causal ? 1 : 0, Q, K, V, O,
+                                    scale, stream);
+}
+
+int pyc_cutlass_attention_dispatch(const char* symbol, int seq_len, int d_head, const void* Q,
+                                   const void* K, const void* V, void* Out, float scale,
+                                   void* stream) {
+    /* Reference ABI: one head, no causal flag (reference cuda_backend.h:128-138). */
+    return pyc_hip_attention_dispatch(symbol, 1, 1, seq_len, d_head, 0, Q, K, V, Out, scale, stream) == 0 ? 0 : -1;
+}
+
+/* ---------------------------------------------------------------- conv2d */
+
+int pyc_hip_conv2d_dispatch(const char* symbol, int N, int H, int W, int C_in, int K, int R, int S,
+                            int pad_h, int pad_w, int stride_h, int stride_w, const void* x,
+                            const void* w, const float* bias, int relu, void* y, void* stream) {
+    const hip_variant* v = find_variant(symbol, VK_CONV);
+    if (!v || N <= 0 || H <= 0 || W <= 0 || C_in <= 0 || K <= 0 || R <= 0 || S <= 0 || !x || !w || !y) {
+        return -1;
+    }
+    if (pad_h < 0 || pad_w < 0 || stride_h <= 0 || stride_w <= 0 || (C_in % 8) != 0) {
+        return -1;
+    }
+    if (H + 2 * pad_h < R || W + 2 * pad_w < S) {
+        return -1;
+    }
+    return pyc_hip_conv2d_launch(v->dtype == VT_BF16, N, H, W, C_in, K, R, S, pad_h, pad_w, stride_h,
+                                 stride_w, x, w, bias, relu ? 1 : 0, y, stream);
+}
+
+int pyc_cutlass_conv2d_dispatch(const char* symbol, int N, int H, int W, int C_in, int K, int R, int S,
+                                int pad_h, int pad_w, int stride_h, int stride_w, const void* input,
+                                const void* filter, void* output, void* stream) {
+    return pyc_hip_conv2d_dispatch(symbol, N, H, W, C_in, K, R, S, pad_h, pad_w, stride_h, stride_w,
+                                   input, filter, NULL, 0, output, stream) == 0 ? 0 : -1;
+}
+
+/* ---------------------------------------------------------------- fp8 weight GEMM */
+
+int pyc_hip_w8a16_gemm_dispatch(const char* symbol, int M, int N, int K, const void* X,
+                                const void* Wq, const float* scale, int relu, void* Y, void* stream) {
+    const hip_variant* v = find_variant(symbol, VK_W8);
+    if (!v || M <= 0 || M > 32 || N <= 0 || K <= 0 || (K % 16) != 0 || !X || !Wq || !scale || !Y) {
+        return -1;
+    }
+    return pyc_hip_w8a16_launch(M, N, K, X, Wq, scale, relu ? 1 : 0, Y, stream);
+}
+
+/* ---------------------------------------------------------------- registry */
+
+static pyc_mutex g_registry_init_lock = PYC_MUTEX_INIT;
+static int g_registry_initialized = 0;
+
+/* Registers every variant under PYC_BACKEND_CUDA (the GPU backend slot) with
+ * its LDS footprint, MFMA eligibility and CDNA4 preference, then honours
+ * PYC_PROMOTED_GEMM_SYMBOL (reference registry/init.cu:32-78). */
+void pyc_cutlass_registry_init(void) {
+    size_t i;
+    pyc_mutex_lock(&g_registry_init_lock);
+    if (!g_registry_initialized) {
+        const char* promoted = getenv("PYC_PROMOTED_GEMM_SYMBOL");
+        g_registry_initialized = 1;
+        for (i = 0; i < sizeof(k_variants) / sizeof(k_variants[0]); ++i) {
+            const hip_variant* v = &k_variants[i];
+            pyc_kernel_desc d;
+            memset(&d, 0, sizeof(d));
+            strncpy(d.op_key, v->op_key, sizeof(d.op_key) - 1);
+            strncpy(d.symbol, v->symbol, sizeof(d.symbol) - 1);
+            d.backend = PYC_BACKEND_CUDA;
+            d.priority = v->priority;
+            d.estimated_occupancy = v->occupancy;
+            d.tensor_core_eligible = 1;
+            d.shared_mem_bytes = v->lds_bytes;
+            d.reg_pressure_class = v->reg_class;
+            d.preferred_workload_family = v->workload;
+            d.preferred_hardware_family = PYC_KERNEL_HARDWARE_CDNA4;
+            (void)pyc_kernel_register(&d);
+        }
+        if (promoted && promoted[0] != '\0') {
+            (void)pyc_kernel_promote_symbol("matmul", PYC_BACKEND_CUDA, promoted);
+        }
+    }
+    pyc_mutex_unlock(&g_registry_init_lock);
+}
+
+/* Registration at library load, as the reference's constructor does
+ * (reference registry/init.cu:80-83). */
+__attribute__((constructor)) static void pyc_hip_registry_autoinit(void) {
+    pyc_cutlass_registry_init();
+}
+
+int pyc_cutlass_kernel_count(const char* op_key) {
+    pyc_kernel_desc descs[64];
+    return (int)pyc_kernel_collect(op_key, PYC_BACKEND_CUDA, descs, 64);
+}
+
+/* ---------------------------------------------------------------- device info */
+
+int pyc_hip_device_query(pyc_hip_device_info* info) {
+    int dev = 0;
+    int count = 0;
+    hipDeviceProp_t prop;
+    if (!info) {
+        return -1;
+    }
+    memset(info, 0, sizeof(*info));
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
+        return -1;
+    }
+    if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess) {
+        return -1;
+    }
+    strncpy(info->gcn_arch, prop.gcnArchName, sizeof(info->gcn_arch) - 1);
+    info->compute_units = prop.multiProcessorCount;
+    info->clock_khz = prop.clockRate;
+    info->memory_clock_khz = prop.memoryClockRate;
+    info->memory_bus_width = prop.memoryBusWidth;
+    info->total_global_mem = prop.totalGlobalMem;
+    info->lds_per_block = prop.sharedMemPerBlock;
+    info->xcds = strncmp(prop.gcnArchName, "gfx950", 6) == 0 || strncmp(prop.gcnArchName, "gfx942", 6) == 0 ? 8 : 1;
+    return 0;
+}

@@ -1,0 +1,61 @@
+// common.hpp — shared device-side types and helpers for the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pyc {
+
+typedef __bf16 bf16_t;
+typedef _Float16 f16_t;
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
+typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2;
+
+constexpr int kWave = 64;
+
+// Element traits: storage type is always a 16-bit pattern for the half types.
+template <typename T> struct elem;
+template <> struct elem<bf16_t> {
+    static constexpr int kBytes = 2;
+    __device__ static inline float to_f32(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
+    // Round to nearest even; NaN stays a quiet NaN.
+    __device__ static inline uint16_t from_f32(float f) {
+        uint32_t u = __float_as_uint(f);
+        if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40u);
+        u += 0x7fffu + ((u >> 16) & 1u);
+        return (uint16_t)(u >> 16);
+    }
+};
+template <> struct elem<f16_t> {
+    static constexpr int kBytes = 2;
+    __device__ static inline float to_f32(uint16_t h) {
+        f16_t v;
+        __builtin_memcpy(&v, &h, 2);
+        return (float)v;
+    }
+    __device__ static inline uint16_t from_f32(float f) {
+        f16_t v = (f16_t)f;
+        uint16_t h;
+        __builtin_memcpy(&h, &v, 2);
+        return h;
+    }
+};
+
+// One 16x16x32 MFMA with fp32 accumulation on 8 half-precision k values per lane.
+__device__ inline f32x4 mfma16x16x32(const u32x4& a, const u32x4& b, const f32x4& c, bf16_t) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+__device__ inline f32x4 mfma16x16x32(const u32x4& a, const u32x4& b, const f32x4& c, f16_t) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                 __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+__device__ inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+}  // namespace pyc

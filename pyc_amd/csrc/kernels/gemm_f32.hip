@@ -1,0 +1,172 @@
+// gemm_f32.hip — true-fp32 GEMM on gfx950 MFMA (v_mfma_f32_16x16x4_f32).
+//
+// The fp32 lane of the run path: C[M,N] = epi(alpha*A[M,K]*op(B) + beta*C) with
+// fp32 inputs, fp32 products and fp32 accumulation (no TF32 / xf32 rounding of
+// the inputs; the reference's cuBLAS lane defaulted to TF32,
+// reference src/compiler/runtime/cuda_backend.c:728-738). Replaces
+// cutlass_gemm_simt_f32 and ada_gemm_k64_warp32_async_f32
+// (reference gemm/kernel.cu:89-99, gemm/ada_async_kernel.cu:150-320), and fuses
+// the row-bias + ReLU epilogue the reference ran on the host after the copy
+// back (reference cuda_backend.c:1697-1742).
+//
+// Tile 64x64x32, 4 waves (2x2) of 32x32; each lane reads 4 consecutive k of
+// its row as one 16-byte LDS load and issues 4 MFMAs, one per element, so A
+// and B use the same k permutation {4*(lane/16)+e}. B is staged in LDS as
+// [n][k] for both layouts ([K,N] tiles are transposed on the LDS store).
+#include "common.hpp"
+
+namespace pyc {
+
+constexpr int kF32BM = 64;
+constexpr int kF32BN = 64;
+constexpr int kF32BK = 32;
+constexpr int kF32Ch = kF32BK / 4;  // 16-byte chunks per LDS row (8)
+
+__device__ inline int swz8(int row, int chunk) { return chunk ^ (row & 7); }
+
+template <bool BT, bool GUARD>
+__global__ void __launch_bounds__(256, 2)
+gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,
+                int M, int N, int K, float alpha, float beta, const float* __restrict__ bias,
+                int epi) {
+    __shared__ __attribute__((aligned(16))) float As[2][kF32BM * kF32BK];
+    __shared__ __attribute__((aligned(16))) float Bs[2][kF32BN * kF32BK];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave >> 1;
+    const int wn = wave & 1;
+    const int m0 = blockIdx.y * kF32BM;
+    const int n0 = blockIdx.x * kF32BN;
+    const bool vec_k = (K & 3) == 0;
+    const bool vec_n = (N & 3) == 0;
+
+    // 64 rows x 8 chunks = 512 chunks per operand tile -> 2 per thread.
+    f32x4 ra[2], rb[2];
+
+    auto ld4 = [&](const float* base, int r, int rmax, int c, int cmax, bool vec, size_t ld) -> f32x4 {
+        if (!GUARD) return *reinterpret_cast<const f32x4*>(base + (size_t)r * ld + c);
+        if (r < rmax && vec && c + 4 <= cmax) return *reinterpret_cast<const f32x4*>(base + (size_t)r * ld + c);
+        f32x4 v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = (r < rmax && c + j < cmax) ? base[(size_t)r * ld + c + j] : 0.f;
+        return v;
+    };
+    auto load = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int q = tid + i * 256;
+            const int row = q >> 3, ch = q & 7;
+            ra[i] = ld4(A, m0 + row, M, k0 + ch * 4, K, vec_k, (size_t)K);
+            if (BT) {
+                rb[i] = ld4(B, n0 + row, N, k0 + ch * 4, K, vec_k, (size_t)K);
+            } else {
+                // [K,N] tile: 32 k rows x 16 chunks of 4 columns.
+                const int kr = q >> 4, nc = q & 15;
+                rb[i] = ld4(B, k0 + kr, K, n0 + nc * 4, N, vec_n, (size_t)N);
+            }
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int q = tid + i * 256;
+            const int row = q >> 3, ch = q & 7;
+            *reinterpret_cast<f32x4*>(&As[buf][row * kF32BK + swz8(row, ch) * 4]) = ra[i];
+            if (BT) {
+                *reinterpret_cast<f32x4*>(&Bs[buf][row * kF32BK + swz8(row, ch) * 4]) = rb[i];
+            } else {
+                const int kr = q >> 4, nc = q & 15;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int n = nc * 4 + j;
+                    Bs[buf][n * kF32BK + swz8(n, kr >> 2) * 4 + (kr & 3)] = rb[i][j];
+                }
+            }
+        }
+    };
+
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int ktiles = (K + kF32BK - 1) / kF32BK;
+    load(0);
+    store(0);
+    __syncthreads();
+    const int lrow = lane & 15, lgrp = lane >> 4;
+    for (int kt = 0; kt < ktiles; ++kt) {
+        const int buf = kt & 1;
+        const bool more = kt + 1 < ktiles;
+        if (more) load((kt + 1) * kF32BK);
+#pragma unroll
+        for (int kb = 0; kb < kF32BK / 16; ++kb) {
+            const int ch = kb * 4 + lgrp;
+            f32x4 af[2], bfr[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int r = wm * 32 + i * 16 + lrow;
+                af[i] = *reinterpret_cast<const f32x4*>(&As[buf][r * kF32BK + swz8(r, ch) * 4]);
+                const int n = wn * 32 + i * 16 + lrow;
+                bfr[i] = *reinterpret_cast<const f32x4*>(&Bs[buf][n * kF32BK + swz8(n, ch) * 4]);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][e], bfr[j][e], acc[i][j], 0, 0, 0);
+        }
+        if (more) store(buf ^ 1);
+        __syncthreads();
+    }
+
+    const bool has_bias = (epi & 1) && bias != nullptr;
+    const bool relu = (epi & 2) != 0;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int gn = n0 + wn * 32 + j * 16 + lrow;
+        if (GUARD && gn >= N) continue;
+        const float bv = has_bias ? bias[gn] : 0.f;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int gm = m0 + wm * 32 + i * 16 + lgrp * 4 + r;
+                if (GUARD && gm >= M) continue;
+                float* cp = C + (size_t)gm * N + gn;
+                float v = alpha * acc[i][j][r];
+                if (beta != 0.f) v += beta * *cp;
+                v += bv;
+                if (relu) v = v > 0.f ? v : 0.f;
+                *cp = v;
+            }
+        }
+    }
+}
+
+}  // namespace pyc
+
+extern "C" int pyc_hip_gemm_f32_launch(int b_trans, int M, int N, int K, const void* A,
+                                       const void* B, void* C, float alpha, float beta,
+                                       const float* bias, int epi, void* stream) {
+    using namespace pyc;
+    dim3 grid((N + kF32BN - 1) / kF32BN, (M + kF32BM - 1) / kF32BM), block(256);
+    const bool even = (M % kF32BM == 0) && (N % kF32BN == 0) && (K % kF32BK == 0);
+    hipStream_t s = (hipStream_t)stream;
+    const float* a = (const float*)A;
+    const float* b = (const float*)B;
+    float* c = (float*)C;
+    if (b_trans) {
+        if (even) hipLaunchKernelGGL((gemm_f32_kernel<true, false>), grid, block, 0, s, a, b, c, M, N, K, alpha, beta, bias, epi);
+        else hipLaunchKernelGGL((gemm_f32_kernel<true, true>), grid, block, 0, s, a, b, c, M, N, K, alpha, beta, bias, epi);
+    } else {
+        if (even) hipLaunchKernelGGL((gemm_f32_kernel<false, false>), grid, block, 0, s, a, b, c, M, N, K, alpha, beta, bias, epi);
+        else hipLaunchKernelGGL((gemm_f32_kernel<false, true>), grid, block, 0, s, a, b, c, M, N, K, alpha, beta, bias, epi);
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+}

@@ -1,0 +1,166 @@
+"""GPU parity: MFMA GEMMs (bf16 / fp16 / fp32) against the CPU oracle.
+
+Tolerances:
+  * fp32 GEMM: max|got-ref| / max|ref| <= 1e-4 against the CPU executor;
+  * bf16 / fp16 paths: max|got-ref| <= 2e-2 * max|ref| against the fp32 CPU
+    result; additionally every element must sit within one output rounding
+    (2^-8 relative for bf16) plus a K-dependent accumulation-order term, which
+    a dropped k-tile or a transposed operand would break.
+"""
+import numpy as np
+import pytest
+
+import oracle
+import pyc_amd
+from tests.gpu_util import dev_bits16, dev_f32, host_bits16, rel_max_err
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 2e-2
+F32_TOL = 1e-4
+
+
+def _bf16_inputs(m, n, k, seed, b_trans):
+    r = np.random.default_rng(seed)
+    a = oracle.f32_to_bf16((r.standard_normal((m, k)) / np.sqrt(k)).astype(np.float32))
+    shape = (n, k) if b_trans else (k, n)
+    b = oracle.f32_to_bf16(r.standard_normal(shape).astype(np.float32))
+    return a, b
+
+
+def _check_half(got_bits, ref, k):
+    got = oracle.bf16_to_f32(got_bits)
+    assert rel_max_err(got, ref) <= BF16_TOL
+    bound = 2.0 ** -8 * np.abs(ref) + 4e-6 * np.sqrt(k) * np.abs(ref).max()
+    bad = np.abs(got - ref) > bound
+    assert not bad.any(), f"{bad.sum()} elements off, first at {np.argwhere(bad)[0]}"
+
+
+SHAPES = [(256, 256, 64), (512, 768, 256), (300, 200, 72), (1, 1, 8), (33, 65, 40),
+          (1024, 1024, 1024), (130, 257, 520)]
+
+
+@pytest.mark.parametrize("m,n,k", SHAPES)
+@pytest.mark.parametrize("layout", ["nt", "nn"])
+@pytest.mark.parametrize("tile", ["", "_128x128", "_256x256"])
+def test_bf16_gemm_vs_oracle(gpu, m, n, k, layout, tile):
+    torch = gpu
+    bt = layout == "nt"
+    a, b = _bf16_inputs(m, n, k, m * 7 + n + k, bt)
+    A, B = dev_bits16(torch, a), dev_bits16(torch, b)
+    Cd = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    pyc_amd.gemm(f"hip_gemm_bf16_{layout}{tile}", A, B, Cd, m, n, k)
+    torch.cuda.synchronize()
+    _check_half(host_bits16(Cd), oracle.gemm_bf16(a, b, bt, threads=8), k)
+
+
+def test_bf16_gemm_8192_sampled_rows(gpu):
+    """Config 2 at full size: every row block of the GPU result is checked on a
+    row sample (rows spread over all 32 tile rows) against the oracle."""
+    torch = gpu
+    m = n = k = 8192
+    g = torch.Generator(device="cuda").manual_seed(1)
+    A = (torch.randn((m, k), generator=g, device="cuda") / np.sqrt(k)).to(torch.bfloat16)
+    g2 = torch.Generator(device="cuda").manual_seed(2)
+    B = (torch.randn((n, k), generator=g2, device="cuda") / np.sqrt(k)).to(torch.bfloat16)
+    Cd = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    pyc_amd.gemm("hip_gemm_bf16_nt", A, B, Cd, m, n, k)
+    torch.cuda.synchronize()
+    rows = np.unique(np.concatenate([np.arange(0, m, 257), [m - 1]]))
+    a = host_bits16(A[torch.from_numpy(rows).cuda()])
+    b = host_bits16(B)
+    ref = oracle.gemm_bf16(a, b, True, threads=16)
+    _check_half(host_bits16(Cd[torch.from_numpy(rows).cuda()]), ref, k)
+    # size-independent property: the column sums of C equal (1^T A) B^T up to rounding
+    colsum = Cd.float().sum(0).double()
+    pred = (A.double().sum(0, keepdim=True) @ B.double().t()).squeeze(0)
+    assert (colsum - pred).abs().max().item() <= 1e-2 * pred.abs().max().item()
+
+
+@pytest.mark.parametrize("layout", ["nt", "nn"])
+def test_bf16_gemm_epilogue(gpu, layout):
+    torch = gpu
+    m, n, k = 192, 320, 136
+    bt = layout == "nt"
+    a, b = _bf16_inputs(m, n, k, 5, bt)
+    r = np.random.default_rng(6)
+    c0 = oracle.f32_to_bf16(r.standard_normal((m, n)).astype(np.float32))
+    bias = r.standard_normal(n).astype(np.float32)
+    A, B = dev_bits16(torch, a), dev_bits16(torch, b)
+    Cd = dev_bits16(torch, c0.copy())
+    pyc_amd.gemm(f"hip_gemm_bf16_{layout}", A, B, Cd, m, n, k, alpha=0.5, beta=-1.25,
+                 bias=dev_f32(torch, bias), epilogue=pyc_amd.abi.EPI_BIAS | pyc_amd.abi.EPI_RELU)
+    torch.cuda.synchronize()
+    ref = np.maximum(0.5 * oracle.gemm_bf16(a, b, bt) - 1.25 * oracle.bf16_to_f32(c0) + bias, 0)
+    _check_half(host_bits16(Cd), ref, k)
+
+
+def test_f16_gemm(gpu):
+    torch = gpu
+    m, n, k = 200, 136, 264
+    r = np.random.default_rng(21)
+    a = (r.standard_normal((m, k)) / np.sqrt(k)).astype(np.float16)
+    b = r.standard_normal((n, k)).astype(np.float16)
+    A = torch.from_numpy(a).cuda()
+    B = torch.from_numpy(b).cuda()
+    Cd = torch.empty((m, n), dtype=torch.float16, device="cuda")
+    pyc_amd.gemm("hip_gemm_f16_nt", A, B, Cd, m, n, k)
+    torch.cuda.synchronize()
+    ref = oracle.matmul_f32(a.astype(np.float32), np.ascontiguousarray(b.astype(np.float32).T))
+    got = Cd.float().cpu().numpy()
+    assert rel_max_err(got, ref) <= BF16_TOL
+    assert np.all(np.abs(got - ref) <= 2.0 ** -10 * np.abs(ref) + 1e-5 * np.sqrt(k) * np.abs(ref).max())
+
+
+def test_config1_f32_gemm_bias_relu(gpu):
+    """Config 1: X[1024x1024] @ W[1024x1024] + bias[1024] -> ReLU, U(-1,1) seed 0."""
+    torch = gpu
+    r = np.random.default_rng(0)
+    x = r.uniform(-1, 1, (1024, 1024)).astype(np.float32)
+    w = r.uniform(-1, 1, (1024, 1024)).astype(np.float32)
+    bias = r.uniform(-1, 1, 1024).astype(np.float32)
+    X, W, Bv = dev_f32(torch, x), dev_f32(torch, w), dev_f32(torch, bias)
+    Y = torch.empty((1024, 1024), dtype=torch.float32, device="cuda")
+    pyc_amd.gemm("hip_gemm_f32_nn_64x64", X, W, Y, 1024, 1024, 1024, bias=Bv,
+                 epilogue=pyc_amd.abi.EPI_BIAS | pyc_amd.abi.EPI_RELU)
+    torch.cuda.synchronize()
+    ref = oracle.gemm_bias_relu_f32(x, w, bias, relu=True, threads=8)
+    assert rel_max_err(Y.cpu().numpy(), ref) <= F32_TOL
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 1, 1), (5, 7, 3), (64, 64, 32), (100, 70, 50), (257, 129, 65)])
+@pytest.mark.parametrize("symbol,bt", [("hip_gemm_f32_nn_64x64", False), ("hip_gemm_f32_nt_64x64", True),
+                                       ("cutlass_gemm_simt_f32", True),
+                                       ("ada_gemm_k64_warp32_async_f32", False)])
+def test_f32_gemm_shapes(gpu, m, n, k, symbol, bt):
+    torch = gpu
+    r = np.random.default_rng(m + n + k)
+    a = r.uniform(-1, 1, (m, k)).astype(np.float32)
+    b = r.uniform(-1, 1, (n, k) if bt else (k, n)).astype(np.float32)
+    Cd = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    pyc_amd.gemm(symbol, dev_f32(torch, a), dev_f32(torch, b), Cd, m, n, k)
+    torch.cuda.synchronize()
+    ref = oracle.matmul_f32(a, np.ascontiguousarray(b.T) if bt else b)
+    assert rel_max_err(Cd.cpu().numpy(), ref) <= F32_TOL
+
+
+def test_reference_symbols_and_rejections(gpu):
+    torch = gpu
+    L = pyc_amd.lib()
+    m = n = k = 128
+    a, b = _bf16_inputs(m, n, k, 3, False)
+    A, B = dev_bits16(torch, a), dev_bits16(torch, b)
+    Cd = torch.zeros((m, n), dtype=torch.bfloat16, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    # reference default bf16 symbol: all operands row-major (NN)
+    assert L.pyc_cutlass_gemm_dispatch(b"cutlass_gemm_tensorcore_bf16", m, n, k, A.data_ptr(),
+                                       B.data_ptr(), Cd.data_ptr(), 1.0, 0.0, s) == 0
+    torch.cuda.synchronize()
+    _check_half(host_bits16(Cd), oracle.gemm_bf16(a, b, False), k)
+    assert L.pyc_cutlass_gemm_dispatch(b"no_such_kernel", m, n, k, A.data_ptr(), B.data_ptr(),
+                                       Cd.data_ptr(), 1.0, 0.0, s) == -1
+    # the async fp32 kernel accepts alpha=1, beta=0 only (reference ada_async_kernel.cu:285-287)
+    assert L.pyc_cutlass_gemm_dispatch(b"ada_gemm_k64_warp32_async_f32", m, n, k, A.data_ptr(),
+                                       B.data_ptr(), Cd.data_ptr(), 1.0, 1.0, s) == -1
+    assert L.pyc_hip_gemm_dispatch(b"hip_gemm_bf16_nt", 0, n, k, A.data_ptr(), B.data_ptr(),
+                                   Cd.data_ptr(), 1.0, 0.0, None, 0, s) == -1

@@ -1,0 +1,302 @@
+"""Pins the CPU oracle (oracle/oracle.c) before anything is checked against it.
+
+Each oracle function is checked against something it did not compute itself:
+the reference's own known-answer tests, the reference engine built from its
+sources (oracle/_ref), independent library routines (numpy fp64, torch dtype
+conversions and scaled_dot_product_attention, scipy.signal.correlate) and
+mathematical invariants chosen so that a dropped term, a wrong index or a
+transposed operand fails.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from tests import refengine
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+# ---------------------------------------------------------------- CPU executor GEMM
+
+
+def test_matmul_kat_reference_cpu_execution():
+    # reference tests/compiler_next/test_cpu_execution.c:56-59
+    a = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
+    b = np.array([[7, 8], [9, 10], [11, 12]], np.float32)
+    np.testing.assert_array_equal(oracle.matmul_f32(a, b), [[58, 64], [139, 154]])
+    a = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
+    b = np.array([[1, 2], [3, 4], [5, 6]], np.float32)
+    np.testing.assert_array_equal(oracle.matmul_f32(a, b), [[22, 28], [49, 64]])
+
+
+def test_matmul_bias_relu_kat_reference_cuda_backend():
+    # reference tests/compiler_next/test_cuda_backend.c:84-89
+    lhs = np.array([[1, -2], [3, 4]], np.float32)
+    rhs = np.array([[2, 1], [-1, 3]], np.float32)
+    bias = np.array([0.5, -1.5], np.float32)
+    out = oracle.gemm_bias_relu_f32(lhs, rhs, bias, relu=True)
+    np.testing.assert_allclose(out, [[4.5, 0.0], [2.5, 13.5]], atol=1e-5)
+
+
+def test_add_relu_kat_reference_cpu_execution():
+    # reference tests/compiler_next/test_cpu_execution.c:135-138 (flat add + relu)
+    a = np.array([[-1, 2, -3, 4]], np.float32)
+    b = np.array([[2, -5, 4, -1]], np.float32)
+    out = a.copy()
+    oracle.add_epilogue(out, b, 1)
+    oracle.relu_(out)
+    np.testing.assert_array_equal(out, [[1, 0, 1, 3]])
+
+
+def test_add_modes_broadcast():
+    out = np.zeros((3, 4), np.float32)
+    oracle.add_epilogue(out, np.arange(4, dtype=np.float32), 2)
+    np.testing.assert_array_equal(out, np.tile(np.arange(4, dtype=np.float32), (3, 1)))
+    out = np.zeros((3, 4), np.float32)
+    oracle.add_epilogue(out, np.array([2.5], np.float32), 3)
+    np.testing.assert_array_equal(out, np.full((3, 4), 2.5, np.float32))
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 1, 1), (7, 13, 5), (64, 64, 64), (33, 130, 17)])
+def test_matmul_against_fp64(m, k, n):
+    r = rng(m * 1000 + k)
+    a = r.uniform(-1, 1, (m, k)).astype(np.float32)
+    b = r.uniform(-1, 1, (k, n)).astype(np.float32)
+    got = oracle.matmul_f32(a, b)
+    ref = a.astype(np.float64) @ b.astype(np.float64)
+    assert np.abs(got - ref).max() <= 1e-6 * k * max(1.0, np.abs(ref).max())
+
+
+def test_matmul_sequential_k_order():
+    # sequential fp32 accumulation is not associative: (1e8 + 1) - 1e8 = 0 in fp32
+    # when k ascends; a reordered or fp64 sum would give 1.
+    a = np.array([[1e8, 1.0, -1e8]], np.float32)
+    b = np.ones((3, 1), np.float32)
+    assert oracle.matmul_f32(a, b)[0, 0] == 0.0
+    a = np.array([[1e8, -1e8, 1.0]], np.float32)
+    assert oracle.matmul_f32(a, b)[0, 0] == 1.0
+
+
+def test_matmul_threads_do_not_change_bits():
+    r = rng(3)
+    a = r.uniform(-1, 1, (37, 91)).astype(np.float32)
+    b = r.uniform(-1, 1, (91, 29)).astype(np.float32)
+    np.testing.assert_array_equal(oracle.matmul_f32(a, b, 1), oracle.matmul_f32(a, b, 6))
+
+
+@pytest.mark.skipif(not refengine.available(), reason="oracle/_ref not built here")
+@pytest.mark.parametrize("m,k,n", [(2, 3, 2), (64, 64, 64), (48, 200, 33), (9, 1024, 8)])
+def test_matmul_bitexact_vs_reference_engine(m, k, n):
+    r = rng(m + k + n)
+    a = r.uniform(-1, 1, (m, k)).astype(np.float32)
+    b = r.uniform(-1, 1, (k, n)).astype(np.float32)
+    model = refengine.matmul_model(m, k, n)
+    try:
+        st, (out,), stats = model.run([a, b], [(m, n)])
+    finally:
+        model.close()
+    assert st == 0
+    np.testing.assert_array_equal(out, oracle.matmul_f32(a, b))
+
+
+@pytest.mark.skipif(not refengine.available(), reason="oracle/_ref not built here")
+def test_bias_relu_vs_reference_simulated_gpu(monkeypatch):
+    # The reference's simulated GPU executor applies the row-bias broadcast
+    # (reference cuda_backend.c:1556-1568); its naive loop sums k ascending too.
+    monkeypatch.setenv("PYC_CUDA_SIMULATE_AVAILABLE", "1")
+    r = rng(11)
+    m, k, n = 16, 40, 24
+    a = r.uniform(-1, 1, (m, k)).astype(np.float32)
+    b = r.uniform(-1, 1, (k, n)).astype(np.float32)
+    bias = r.uniform(-1, 1, (n,)).astype(np.float32)
+    model = refengine.matmul_model(m, k, n, bias=(n,), relu=True, backend=1)
+    try:
+        st, (out,), stats = model.run([a, b, bias], [(m, n)])
+        assert "cuda_fallback=0" in model.log()
+    finally:
+        model.close()
+    assert st == 0
+    np.testing.assert_array_equal(out, oracle.gemm_bias_relu_f32(a, b, bias, relu=True))
+
+
+# ---------------------------------------------------------------- bf16 / fp8 codecs
+
+
+def test_bf16_roundtrip_vs_torch():
+    torch = pytest.importorskip("torch")
+    r = rng(5)
+    x = np.concatenate([
+        r.normal(0, 1, 4096).astype(np.float32),
+        r.normal(0, 1e-38, 256).astype(np.float32),  # subnormals
+        np.array([0.0, -0.0, np.inf, -np.inf, 3.4e38, -3.4e38], np.float32),
+        # exact ties: 1 + 2^-8 (round down to even), 1 + 3*2^-8 (round up to even)
+        np.array([1.00390625, 1.01171875, -1.00390625], np.float32),
+    ])
+    got = oracle.f32_to_bf16(x)
+    ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(got, ref)
+    back = oracle.bf16_to_f32(got)
+    np.testing.assert_array_equal(back, torch.from_numpy(ref.view(np.int16)).view(torch.bfloat16).float().numpy())
+    nan = oracle.f32_to_bf16(np.array([np.nan], np.float32))
+    assert np.isnan(oracle.bf16_to_f32(nan))[0]
+
+
+def test_e4m3_decode_all_codes_vs_torch():
+    torch = pytest.importorskip("torch")
+    table = oracle.e4m3_table()
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8)
+    ref = codes.view(torch.float8_e4m3fn).float().numpy()
+    nan_mask = np.isnan(ref)
+    assert nan_mask.sum() == 2  # 0x7F and 0xFF
+    np.testing.assert_array_equal(np.isnan(table), nan_mask)
+    np.testing.assert_array_equal(table[~nan_mask], ref[~nan_mask])
+    assert table[0x7E] == 448.0 and table[0x08] == 2.0 ** -6 and table[0x01] == 2.0 ** -9
+
+
+def test_e4m3_encode_vs_torch_in_range():
+    torch = pytest.importorskip("torch")
+    r = rng(6)
+    x = np.concatenate([
+        r.uniform(-448, 448, 3000), r.normal(0, 1, 2000), r.normal(0, 0.01, 1000),
+        # midpoints between neighbouring codes exercise round-half-even
+        (oracle.e4m3_table()[1:0x7E] + oracle.e4m3_table()[2:0x7F]) / 2,
+    ]).astype(np.float32)
+    got = oracle.f32_to_e4m3(x)
+    ref = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(got, ref)
+
+
+def test_e4m3_saturates():
+    got = oracle.f32_to_e4m3(np.array([449.0, 1e6, -1e6, 464.0], np.float32))
+    np.testing.assert_array_equal(got, [0x7E, 0x7E, 0xFE, 0x7E])
+
+
+def test_quantize_per_col_roundtrip():
+    r = rng(7)
+    w = r.normal(0, 0.02, (64, 48)).astype(np.float32)
+    wq, scale = oracle.quantize_e4m3_per_col(w)
+    deq = oracle.e4m3_table()[wq].T * scale  # [K,N]
+    # every column's max maps to 448 exactly; relative error bounded by 2^-4
+    np.testing.assert_allclose(np.abs(deq).max(axis=0), np.abs(w).max(axis=0), rtol=1e-6)
+    big = np.abs(w) > 2.0 ** -6 * scale
+    assert np.all(np.abs(deq - w)[big] <= 2.0 ** -4 * np.abs(w)[big] + 1e-12)
+
+
+# ---------------------------------------------------------------- bf16 GEMM
+
+
+def test_gemm_bf16_vs_fp64_and_layouts():
+    r = rng(8)
+    m, n, k = 40, 24, 96
+    a = oracle.f32_to_bf16(r.normal(0, 1, (m, k)).astype(np.float32))
+    bt = oracle.f32_to_bf16(r.normal(0, 1, (n, k)).astype(np.float32))  # [N,K]
+    b = np.ascontiguousarray(bt.T)  # [K,N]
+    ref = oracle.bf16_to_f32(a).astype(np.float64) @ oracle.bf16_to_f32(b).astype(np.float64)
+    nt = oracle.gemm_bf16(a, bt, True)
+    nn = oracle.gemm_bf16(a, b, False)
+    np.testing.assert_array_equal(nt, nn)
+    assert np.abs(nt - ref).max() <= 1e-5 * np.abs(ref).max()
+    rows = oracle.gemm_bf16(a, bt, True, rows=(8, 20))
+    np.testing.assert_array_equal(rows, nt[8:20])
+
+
+# ---------------------------------------------------------------- attention
+
+
+def _sdpa64(q, k, v, causal, scale):
+    torch = pytest.importorskip("torch")
+    f = torch.nn.functional.scaled_dot_product_attention
+    t = lambda x: torch.from_numpy(x.astype(np.float64))
+    return f(t(q), t(k), t(v), is_causal=causal, scale=scale).numpy()
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_vs_torch_sdpa_fp64(causal):
+    r = rng(9)
+    q, k, v = (r.normal(0, 1, (2, 3, 37, 16)).astype(np.float32) for _ in range(3))
+    got = oracle.attention_f32(q, k, v, causal, 0.25)
+    np.testing.assert_allclose(got, _sdpa64(q, k, v, causal, 0.25), atol=2e-6, rtol=1e-5)
+
+
+def test_attention_invariants():
+    r = rng(10)
+    q, k, v = (r.normal(0, 1, (1, 2, 20, 8)).astype(np.float32) for _ in range(3))
+    o = oracle.attention_f32(q, k, v, True, 0.3)
+    np.testing.assert_allclose(o[:, :, 0], v[:, :, 0], rtol=1e-6)  # row 0 sees only key 0
+    cv = np.broadcast_to(r.normal(0, 1, (1, 2, 1, 8)), v.shape).astype(np.float32).copy()
+    np.testing.assert_allclose(oracle.attention_f32(q, k, cv, True, 0.3), cv, rtol=1e-5)
+    o0 = oracle.attention_f32(q, k, v, True, 0.0)  # uniform weights: causal prefix mean
+    prefix = np.cumsum(v.astype(np.float64), axis=2) / np.arange(1, 21)[None, None, :, None]
+    np.testing.assert_allclose(o0, prefix, rtol=1e-5, atol=1e-6)
+
+
+def test_attention_bh_slice():
+    r = rng(12)
+    q, k, v = (r.normal(0, 1, (2, 2, 9, 8)).astype(np.float32) for _ in range(3))
+    full = oracle.attention_f32(q, k, v, True, 0.5)
+    part = oracle.attention_f32(q, k, v, True, 0.5, bh=(1, 3))
+    np.testing.assert_array_equal(part.reshape(4, 9, 8)[1:3], full.reshape(4, 9, 8)[1:3])
+    assert not part.reshape(4, 9, 8)[0].any()
+
+
+# ---------------------------------------------------------------- conv2d
+
+
+@pytest.mark.parametrize("pad,stride", [((1, 1), (1, 1)), ((0, 0), (1, 1)), ((2, 1), (2, 3))])
+def test_conv_vs_scipy(pad, stride):
+    scipy_signal = pytest.importorskip("scipy.signal")
+    r = rng(13)
+    N, H, W, Cin, K, R, S = 2, 9, 11, 8, 5, 3, 3
+    x = r.uniform(0, 1, (N, H, W, Cin)).astype(np.float32)
+    w = r.normal(0, 0.2, (K, R, S, Cin)).astype(np.float32)
+    bias = r.normal(0, 0.1, (K,)).astype(np.float32)
+    got = oracle.conv2d_nhwc_f32(x, w, bias, pad, stride, relu=False)
+    ph, pw = pad
+    sh, sw = stride
+    xp = np.pad(x.astype(np.float64), ((0, 0), (ph, ph), (pw, pw), (0, 0)))
+    for n in range(N):
+        for kk in range(K):
+            full = scipy_signal.correlate(xp[n], w[kk].astype(np.float64), mode="valid")[:, :, 0]
+            ref = full[::sh, ::sw] + bias[kk]
+            np.testing.assert_allclose(got[n, :, :, kk], ref, rtol=1e-5, atol=1e-5)
+
+
+def test_conv_1x1_is_gemm_and_relu():
+    r = rng(14)
+    x = r.normal(0, 1, (2, 5, 6, 16)).astype(np.float32)
+    w = r.normal(0, 1, (7, 1, 1, 16)).astype(np.float32)
+    got = oracle.conv2d_nhwc_f32(x, w, None, (0, 0), (1, 1), relu=True)
+    ref = np.maximum(x.reshape(-1, 16).astype(np.float64) @ w.reshape(7, 16).T.astype(np.float64), 0)
+    np.testing.assert_allclose(got.reshape(-1, 7), ref, rtol=1e-5, atol=1e-5)
+
+
+def test_conv_delta_filter_shifts():
+    r = rng(15)
+    x = r.normal(0, 1, (1, 6, 7, 8)).astype(np.float32)
+    w = np.zeros((8, 3, 3, 8), np.float32)
+    for c in range(8):
+        w[c, 0, 2, c] = 1.0  # tap (r=0, s=2): y[p,q] = x[p-1, q+1]
+    y = oracle.conv2d_nhwc_f32(x, w, None, (1, 1), (1, 1), relu=False)
+    xp = np.pad(x, ((0, 0), (1, 1), (1, 1), (0, 0)))
+    np.testing.assert_array_equal(y[0], xp[0, 0:6, 2:9])
+
+
+# ---------------------------------------------------------------- fp8 decode layer
+
+
+def test_w8a16_layer_vs_fp64():
+    torch = pytest.importorskip("torch")
+    r = rng(16)
+    M, K, N = 5, 64, 24
+    x = oracle.f32_to_bf16(r.normal(0, 1, (M, K)).astype(np.float32))
+    w = r.normal(0, 0.05, (K, N)).astype(np.float32)
+    wq, scale = oracle.quantize_e4m3_per_col(w)
+    wdeq = torch.from_numpy(wq).view(torch.float8_e4m3fn).double().numpy()  # [N,K]
+    ref = (oracle.bf16_to_f32(x).astype(np.float64) @ wdeq.T) * scale[None, :].astype(np.float64)
+    for relu in (False, True):
+        got = oracle.bf16_to_f32(oracle.w8a16_layer(x, wq, scale, relu))
+        exp = np.maximum(ref, 0) if relu else ref
+        # one bf16 rounding of the result: half an ulp, 2^-9 relative
+        np.testing.assert_allclose(got, exp, rtol=2.0 ** -8, atol=1e-6)
