@@ -77,6 +77,14 @@ def load_traffic(name: str):
 # ---------------------------------------------------------------- CPU baseline
 
 
+def _host_cores() -> int:
+    """Cores this process may run on (the GPU box pins a CPU share)."""
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
 def cpu_baseline_gemm(a_rows_f32: np.ndarray, b_kn_f32: np.ndarray, full_flops: float, sample_desc: str):
     """Time the reference CPU executor on a[rows] @ b (fp32) and scale to the
     metric's unit (TFLOP/s on the full workload's FLOP count; the per-row cost
@@ -84,7 +92,7 @@ def cpu_baseline_gemm(a_rows_f32: np.ndarray, b_kn_f32: np.ndarray, full_flops: 
     rows, k = a_rows_f32.shape
     n = b_kn_f32.shape[1]
     flops = 2.0 * rows * k * n
-    threads = min(os.cpu_count() or 1, 32)
+    threads = min(_host_cores(), 32)
     try:
         from tests import refengine
         use_ref = refengine.available()
@@ -255,7 +263,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="gemm_bf16", choices=sorted(WORKLOADS))
     ap.add_argument("--symbol", default=None, help="GEMM kernel symbol override")
-    ap.add_argument("--cpu-rows", type=int, default=64)
+    ap.add_argument("--cpu-rows", type=int, default=1024,
+                    help="rows of the GEMM the CPU executor computes (about 10-30 CPU-seconds)")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
