@@ -253,7 +253,73 @@ def wl_decode_chain(torch, args):
     }
 
 
-WORKLOADS = {"gemm_bf16": wl_gemm_bf16, "gemm_f32_cfg1": wl_gemm_f32_cfg1, "decode_chain": wl_decode_chain}
+def wl_attention(torch, args):
+    """Config 3: causal attention [8,32,2048,128] bf16, scale 1/sqrt(128)."""
+    import pyc_amd
+    B, H, S, D = 8, 32, 2048, 128
+    gens = [torch.Generator(device="cuda").manual_seed(s) for s in (3, 4, 5)]
+    Q, K, V = (torch.randn((B, H, S, D), generator=g, device="cuda").to(torch.bfloat16) for g in gens)
+    O = torch.empty_like(Q)
+    scale = 1.0 / np.sqrt(D)
+    launch = lambda: pyc_amd.attention("hip_attention_bf16", Q, K, V, O, True, scale)  # noqa: E731
+    ms_step, ms_kernel, _ = time_launches(torch, launch, args.steps, args.warmup)
+    flops = 2.0 * B * H * S * S * D  # causal FA convention (half of 4*B*H*S^2*D)
+    res = {
+        "value": flops / (ms_step * 1e-3) / 1e12, "unit": "TFLOP/s", "ms_per_step": ms_step, "dtype": "bf16",
+        "config": {"workload": "attention_causal_bf16_8x32x2048x128", "flop_convention": "2*B*H*S^2*D"},
+        "roofline": {"bound": "mfma", "achieved": flops / (ms_kernel * 1e-3) / 1e12, "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": flops / (ms_kernel * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+                     "traffic": load_traffic("attention_cfg3"), "kernel_ms": ms_kernel},
+    }
+    if not args.no_cpu:
+        import oracle
+        q, k, v = (t[0:1, 0:1].float().cpu().numpy() for t in (Q, K, V))
+        t0 = time.perf_counter()
+        ref = oracle.attention_f32(q, k, v, True, scale)
+        dt = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": 2.0 * S * S * D / dt / 1e12, "unit": "TFLOP/s", "cores": 1,
+                               "kind": "port", "sample": f"1 of {B * H} (b,h) heads, oracle fp32 attention, "
+                                                          f"{dt:.2f} s, extrapolated linearly"}
+        got = O[0:1, 0:1].float().cpu().numpy()
+        res["parity_sample_max_rel_err"] = float(np.abs(got - ref).max() / np.abs(ref).max())
+    return res
+
+
+def wl_conv(torch, args):
+    """Config 4: NHWC conv 32x56x56x256 -> 256, 3x3 s1 p1, + bias + ReLU, bf16."""
+    import pyc_amd
+    N, H, W, C, K = 32, 56, 56, 256, 256
+    gx, gw, gb = (torch.Generator(device="cuda").manual_seed(s) for s in (6, 7, 8))
+    X = torch.rand((N, H, W, C), generator=gx, device="cuda").to(torch.bfloat16)
+    Wd = (torch.randn((K, 3, 3, C), generator=gw, device="cuda") * np.sqrt(2.0 / 2304)).to(torch.bfloat16)
+    Bv = 0.01 * torch.randn(K, generator=gb, device="cuda")
+    Y = torch.empty((N, H, W, K), dtype=torch.bfloat16, device="cuda")
+    launch = lambda: pyc_amd.conv2d("hip_conv2d_bf16", X, Wd, Y, pad=(1, 1), stride=(1, 1), bias=Bv, relu=True)  # noqa: E731
+    ms_step, ms_kernel, _ = time_launches(torch, launch, args.steps, args.warmup)
+    flops = 2.0 * N * H * W * K * C * 9
+    res = {
+        "value": flops / (ms_step * 1e-3) / 1e12, "unit": "TFLOP/s", "ms_per_step": ms_step, "dtype": "bf16",
+        "config": {"workload": "conv2d_nhwc_bf16_32x56x56x256_k256_3x3"},
+        "roofline": {"bound": "mfma", "achieved": flops / (ms_kernel * 1e-3) / 1e12, "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": flops / (ms_kernel * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+                     "traffic": load_traffic("conv_cfg4"), "kernel_ms": ms_kernel},
+    }
+    if not args.no_cpu:
+        import oracle
+        x = X[0:1].float().cpu().numpy()
+        w = Wd.float().cpu().numpy()
+        t0 = time.perf_counter()
+        ref = oracle.conv2d_nhwc_f32(x, w, Bv.cpu().numpy(), (1, 1), (1, 1), True)
+        dt = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": flops / N / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+                               "sample": f"1 of {N} images, oracle direct conv, {dt:.2f} s, extrapolated linearly"}
+        got = Y[0:1].float().cpu().numpy()
+        res["parity_sample_max_rel_err"] = float(np.abs(got - ref).max() / np.abs(ref).max())
+    return res
+
+
+WORKLOADS = {"gemm_bf16": wl_gemm_bf16, "gemm_f32_cfg1": wl_gemm_f32_cfg1, "decode_chain": wl_decode_chain,
+             "attention": wl_attention, "conv": wl_conv}
 
 
 def main() -> int:

@@ -2,7 +2,7 @@
  *
  * Implements the symbol-dispatched entry points the reference exposes for its
  * CUTLASS kernels (reference include/pyc/cuda_backend.h:105-143,
- * src/compiler/cutlass_kernels/{gemm,conv2d,attention,registry}/*.cu) and the
+ * src/compiler/cutlass_kernels/{gemm,conv2d,attention,registry}/ *.cu) and the
  * MI355X extensions declared in pyc/hip_backend.h. Every symbol resolves to a
  * hand-written gfx950 kernel through the variant table below; there is no
  * library GEMM and no CPU path behind these functions.
