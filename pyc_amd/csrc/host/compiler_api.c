@@ -1,0 +1,1658 @@
+/* compiler_api.c — engine lifecycle: pyc_compile_model / pyc_run_model.
+ *
+ * Behaviour of reference src/compiler/compiler_api.c (compile 2318-2657,
+ * run 2659-3266), kept for drop-in callers:
+ *   - compile: verify, option sanitising (rails, distributed, modes), FNV-1a
+ *     fingerprint of the serialised IR, an in-memory compile cache keyed by
+ *     fingerprint + backend + options, the pass pipeline, the default
+ *     "matmul_fused" catalog, speculative plans at input scales 1/2/4, the
+ *     phantom-graph expectation, allocation plan + allocator-aware kernel
+ *     co-selection, optional autotune-DB load, compile decision log;
+ *   - run: stable-repeat fast path, fingerprint / input guards, speculative
+ *     plan lookup, dispatch (CPU executor or the GPU backend through
+ *     pyc_cuda_dispatch), controller tick, kernel re-selection, autotune
+ *     bookkeeping and "op|backend|symbol|best_ms" DB persistence under a
+ *     flock sidecar, run decision log, pyc_run_stats.
+ * Differences, each deliberate:
+ *   - the IR fusion pass never runs on the executed module (the reference
+ *     drops ADD/activation semantics when it does, pass_manager.c:241-267);
+ *     on the GPU the backend fuses bias/ReLU into the kernel epilogue instead;
+ *   - the CPU executor's ADD broadcasts a [N] or [1] operand over rows (the
+ *     reference's flat add reads past the end of a bias, compiler_api.c:1974-2015);
+ *   - on the GPU backend the autotune record of a run is the measured device
+ *     time of the symbol that ran (trace kernel_ms), not a heuristic estimate;
+ *   - PYC_HIP_STRICT=1 turns any CPU fallback of the GPU backend into
+ *     PYC_STATUS_RUNTIME_FAILED (used by the parity tests and the bench);
+ *   - no communicator is ever created (single GPU): distributed options are
+ *     sanitised and recorded only. */
+#include "pyc/compiler_api.h"
+
+#include <fcntl.h>
+#include <math.h>
+#include <pthread.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <sys/file.h>
+#include <time.h>
+#include <unistd.h>
+
+#include "pyc/cuda_backend.h"
+#include "pyc/kernel_registry.h"
+#include "pyc/pass_manager.h"
+#include "pyc/runtime_allocator.h"
+#include "pyc/runtime_control.h"
+#include "pyc_mutex.h"
+
+#define SPEC_MAX 3
+#define SIG_MAX 256
+#define CACHE_MAX 32
+#define CANDIDATE_MAX 32
+#define LOG_MAX 2048
+
+typedef struct {
+    int valid;
+    pyc_objective_mode mode;
+    pyc_ir_module module;
+    pyc_alloc_plan alloc_plan;
+    pyc_kernel_desc selected;
+    pyc_kernel_selection_trace trace;
+    int has_selected;
+    double confidence;
+    char bucket[64];
+    char signature[SIG_MAX];
+} spec_plan;
+
+typedef struct {
+    int enabled;
+    size_t horizon;
+    double confidence;
+    double last_score;
+    size_t matches, mismatches, reshapes;
+    char exp_bucket[64], exp_sig[128], obs_bucket[64], obs_sig[128];
+} phantom_state;
+
+/* Everything a compile produces that a cache hit restores. */
+typedef struct {
+    pyc_ir_module module;
+    pyc_alloc_plan alloc_plan;
+    pyc_kernel_desc selected;
+    pyc_kernel_selection_trace trace;
+    int has_selected;
+    uint64_t fingerprint;
+    pyc_pass_report report;
+    spec_plan spec[SPEC_MAX];
+    size_t spec_count;
+    double spec_confidence;
+    char spec_bucket[64];
+    char spec_signature[SIG_MAX];
+    phantom_state phantom;
+} compiled_artifacts;
+
+struct pyc_compiled_model {
+    pyc_backend backend;
+    pyc_compile_options options;
+    compiled_artifacts art;
+    pyc_runtime_controller controller;
+    pyc_cuda_dispatch_trace trace;
+    uint64_t cache_key;
+    int cache_hit;
+    double compile_ms;
+    int budget_exceeded;
+    int contract_enforced;
+    char autotune_db[512];
+    int autotune_loaded;
+    int autotune_saved;
+    pyc_kernel_desc candidates[CANDIDATE_MAX];
+    size_t candidate_count;
+    size_t run_count;
+    double baseline_ms;
+    double baseline_throughput;
+    size_t guard_misses;
+    size_t fallbacks;
+    size_t spec_misses;
+    size_t spec_guard_misses;
+    /* last run's descriptors (stable-repeat fast path) */
+    int last_valid;
+    uint64_t last_hash;
+    char last_bucket[64];
+    char last_signature[SIG_MAX];
+    pyc_tensor last_in[PYC_IR_MAX_INPUTS];
+    pyc_tensor last_out[PYC_IR_MAX_INPUTS];
+    size_t last_in_count, last_out_count;
+    float* workspace[PYC_IR_MAX_OPS];
+    size_t workspace_bytes[PYC_IR_MAX_OPS];
+    char log[LOG_MAX];
+};
+
+/* ---------------------------------------------------------------- small helpers */
+
+static double now_ms(void) {
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (double)ts.tv_sec * 1e3 + (double)ts.tv_nsec / 1e6;
+}
+
+static int env_on(const char* name) {
+    const char* v = getenv(name);
+    return v && (strcmp(v, "1") == 0 || strcmp(v, "true") == 0 || strcmp(v, "TRUE") == 0);
+}
+
+static int env_on_default(const char* name) {
+    const char* v = getenv(name);
+    if (!v || !v[0]) {
+        return 1;
+    }
+    return !(strcmp(v, "0") == 0 || strcmp(v, "false") == 0 || strcmp(v, "FALSE") == 0);
+}
+
+static void copy_str(char* dst, size_t cap, const char* src) {
+    if (cap == 0) {
+        return;
+    }
+    snprintf(dst, cap, "%s", src ? src : "");
+}
+
+static uint64_t fnv1a(uint64_t h, const void* data, size_t n) {
+    const unsigned char* p = (const unsigned char*)data;
+    size_t i;
+    for (i = 0; i < n; ++i) {
+        h ^= p[i];
+        h *= 1099511628211ULL;
+    }
+    return h;
+}
+
+#define FNV_BASIS 1469598103934665603ULL
+
+static size_t dtype_bytes(pyc_dtype t) {
+    switch (t) {
+        case PYC_DTYPE_F16:
+        case PYC_DTYPE_BF16:
+            return 2;
+        case PYC_DTYPE_I8:
+        case PYC_DTYPE_FP8_E4M3:
+            return 1;
+        case PYC_DTYPE_F32:
+        case PYC_DTYPE_I32:
+            return 4;
+        default:
+            return 0;
+    }
+}
+
+static size_t shape_elems(const pyc_shape* s) {
+    size_t i, n = 1;
+    if (!s || s->rank == 0) {
+        return 0;
+    }
+    for (i = 0; i < s->rank; ++i) {
+        if (s->dims[i] <= 0) {
+            return 0;
+        }
+        n *= (size_t)s->dims[i];
+    }
+    return n;
+}
+
+/* Decision-log builder: appends "key=value" fields, truncating at LOG_MAX. */
+typedef struct {
+    char* buf;
+    size_t cap;
+    size_t used;
+} logbuf;
+
+static void logf_(logbuf* lb, const char* fmt, ...) {
+    va_list ap;
+    int n;
+    if (lb->used + 1 >= lb->cap) {
+        return;
+    }
+    va_start(ap, fmt);
+    n = vsnprintf(lb->buf + lb->used, lb->cap - lb->used, fmt, ap);
+    va_end(ap);
+    if (n < 0) {
+        return;
+    }
+    lb->used = (size_t)n >= lb->cap - lb->used ? lb->cap - 1 : lb->used + (size_t)n;
+}
+
+const char* pyc_status_string(pyc_status status) {
+    switch (status) {
+        case PYC_STATUS_OK: return "OK";
+        case PYC_STATUS_INVALID_ARGUMENT: return "INVALID_ARGUMENT";
+        case PYC_STATUS_VERIFY_FAILED: return "VERIFY_FAILED";
+        case PYC_STATUS_COMPILE_FAILED: return "COMPILE_FAILED";
+        case PYC_STATUS_RUNTIME_FAILED: return "RUNTIME_FAILED";
+        default: return "UNKNOWN";
+    }
+}
+
+/* ---------------------------------------------------------------- fingerprints, buckets */
+
+static int module_fingerprint(const pyc_ir_module* m, uint64_t* out) {
+    enum { CAP = 262144 };
+    char* text = (char*)malloc(CAP);
+    if (!text) {
+        return -1;
+    }
+    if (pyc_ir_serialize(m, text, CAP) != 0) {
+        free(text);
+        return -1;
+    }
+    *out = fnv1a(FNV_BASIS, text, strlen(text));
+    free(text);
+    return 0;
+}
+
+static void bucket_text(size_t bytes, size_t count, char* out, size_t cap) {
+    const char* klass = "unknown";
+    if (bytes > 0 && bytes <= 256) {
+        klass = "tiny";
+    } else if (bytes <= 4096) {
+        klass = "small";
+    } else if (bytes <= 65536) {
+        klass = "medium";
+    } else {
+        klass = "large";
+    }
+    snprintf(out, cap, "%s:i%zu:b%zu", klass, count, bytes);
+}
+
+static int sig_append(char* out, size_t cap, size_t* used, pyc_dtype t, const pyc_shape* s) {
+    size_t d;
+    int n = snprintf(out + *used, cap - *used, "%s%d:r%zu", *used ? ";" : "", (int)t, s->rank);
+    if (n < 0 || (size_t)n >= cap - *used) {
+        return -1;
+    }
+    *used += (size_t)n;
+    for (d = 0; d < s->rank; ++d) {
+        n = snprintf(out + *used, cap - *used, "x%lld", (long long)s->dims[d]);
+        if (n < 0 || (size_t)n >= cap - *used) {
+            return -1;
+        }
+        *used += (size_t)n;
+    }
+    return 0;
+}
+
+static void module_bucket(const pyc_ir_module* m, char* bucket, size_t bcap, char* sig, size_t scap) {
+    size_t i, bytes = 0, count = 0, used = 0;
+    if (sig) {
+        sig[0] = '\0';
+    }
+    for (i = 0; i < m->op_count; ++i) {
+        const pyc_ir_op* op = &m->ops[i];
+        if (op->kind != PYC_IR_OP_INPUT) {
+            continue;
+        }
+        count++;
+        bytes += shape_elems(&op->shape) * dtype_bytes(op->dtype);
+        if (sig && sig_append(sig, scap, &used, op->dtype, &op->shape) != 0) {
+            sig[0] = '\0';
+            sig = NULL;
+        }
+    }
+    if (bucket) {
+        bucket_text(bytes, count, bucket, bcap);
+    }
+}
+
+static void runtime_bucket(const pyc_tensor* in, size_t n, char* bucket, size_t bcap, char* sig, size_t scap) {
+    size_t i, bytes = 0, used = 0;
+    sig[0] = '\0';
+    for (i = 0; i < n; ++i) {
+        const size_t e = shape_elems(&in[i].shape) * dtype_bytes(in[i].dtype);
+        bytes += e ? e : in[i].size_bytes;
+        if (sig && sig_append(sig, scap, &used, in[i].dtype, &in[i].shape) != 0) {
+            sig[0] = '\0';
+            sig = NULL;
+        }
+    }
+    bucket_text(bytes, n, bucket, bcap);
+}
+
+static uint64_t runtime_hash(const pyc_tensor* in, size_t n) {
+    uint64_t h = FNV_BASIS;
+    size_t i, d;
+    for (i = 0; i < n; ++i) {
+        const uint64_t f[3] = {(uint64_t)in[i].dtype, (uint64_t)in[i].size_bytes, (uint64_t)in[i].shape.rank};
+        size_t k;
+        for (k = 0; k < 3; ++k) {
+            h ^= f[k];
+            h *= 1099511628211ULL;
+        }
+        for (d = 0; d < in[i].shape.rank; ++d) {
+            h ^= (uint64_t)in[i].shape.dims[d];
+            h *= 1099511628211ULL;
+        }
+    }
+    return h;
+}
+
+static int same_descriptors(const pyc_tensor* a, size_t na, const pyc_tensor* b, size_t nb) {
+    size_t i, d;
+    if (na != nb) {
+        return 0;
+    }
+    for (i = 0; i < na; ++i) {
+        if (a[i].data != b[i].data || a[i].size_bytes != b[i].size_bytes || a[i].dtype != b[i].dtype ||
+            a[i].shape.rank != b[i].shape.rank) {
+            return 0;
+        }
+        for (d = 0; d < a[i].shape.rank && d < PYC_IR_MAX_DIMS; ++d) {
+            if (a[i].shape.dims[d] != b[i].shape.dims[d]) {
+                return 0;
+            }
+        }
+    }
+    return 1;
+}
+
+/* Input guard (reference compiler_api.c:1343-1413): every INPUT op must get a
+ * tensor of its dtype, shape and at least its byte size, and no extra tensors. */
+static int inputs_match(const pyc_ir_module* m, const pyc_tensor* in, size_t n, char* why, size_t cap) {
+    size_t i, d, seen = 0;
+    copy_str(why, cap, "ok");
+    for (i = 0; i < m->op_count; ++i) {
+        const pyc_ir_op* op = &m->ops[i];
+        size_t need;
+        if (op->kind != PYC_IR_OP_INPUT) {
+            continue;
+        }
+        if (seen >= n) {
+            copy_str(why, cap, "input_count_mismatch");
+            return 0;
+        }
+        if (in[seen].dtype != op->dtype) {
+            copy_str(why, cap, "input_dtype_mismatch");
+            return 0;
+        }
+        if (in[seen].shape.rank != op->shape.rank) {
+            copy_str(why, cap, "input_shape_mismatch");
+            return 0;
+        }
+        for (d = 0; d < op->shape.rank; ++d) {
+            if (in[seen].shape.dims[d] != op->shape.dims[d]) {
+                copy_str(why, cap, "input_shape_mismatch");
+                return 0;
+            }
+        }
+        need = shape_elems(&op->shape) * dtype_bytes(op->dtype);
+        if (need == 0 || in[seen].size_bytes < need) {
+            copy_str(why, cap, "input_size_mismatch");
+            return 0;
+        }
+        seen++;
+    }
+    if (seen != n) {
+        copy_str(why, cap, "input_count_mismatch");
+        return 0;
+    }
+    return 1;
+}
+
+/* GEMM shape class (reference compiler_api.c:1183-1211). */
+static pyc_kernel_workload_family classify(size_t m, size_t n, size_t k) {
+    const size_t hi = m > n ? m : n;
+    const size_t lo = m < n ? m : n;
+    if (m == 0 || n == 0 || k == 0) {
+        return PYC_KERNEL_WORKLOAD_ANY;
+    }
+    if (hi <= 512 || m * n * k <= (size_t)512 * 512 * 512) {
+        return PYC_KERNEL_WORKLOAD_SMALL;
+    }
+    if (m >= 3 * n) {
+        return PYC_KERNEL_WORKLOAD_TALL_SKINNY;
+    }
+    if (n >= 3 * m) {
+        return PYC_KERNEL_WORKLOAD_WIDE_SKINNY;
+    }
+    if (lo >= 1024 && hi <= 2 * lo && k >= 512) {
+        return PYC_KERNEL_WORKLOAD_LARGE_SQUARE;
+    }
+    return PYC_KERNEL_WORKLOAD_SQUARE;
+}
+
+static pyc_kernel_workload_family module_workload(const pyc_ir_module* m, const pyc_tensor* in, size_t n_in) {
+    size_t i, seen = 0;
+    int lhs = -1, rhs = -1;
+    size_t li = (size_t)-1, ri = (size_t)-1;
+    for (i = 0; i < m->op_count; ++i) {
+        if (m->ops[i].kind == PYC_IR_OP_MATMUL && m->ops[i].input_count >= 2) {
+            lhs = m->ops[i].input_ids[0];
+            rhs = m->ops[i].input_ids[1];
+            break;
+        }
+    }
+    if (lhs < 0) {
+        return PYC_KERNEL_WORKLOAD_ANY;
+    }
+    if (!in) {
+        const pyc_shape* a = &m->ops[lhs].shape;
+        const pyc_shape* b = &m->ops[rhs].shape;
+        if (a->rank != 2 || b->rank != 2) {
+            return PYC_KERNEL_WORKLOAD_ANY;
+        }
+        return classify((size_t)a->dims[0], (size_t)b->dims[1], (size_t)a->dims[1]);
+    }
+    for (i = 0; i < m->op_count; ++i) {
+        if (m->ops[i].kind != PYC_IR_OP_INPUT) {
+            continue;
+        }
+        if ((int)i == lhs) {
+            li = seen;
+        }
+        if ((int)i == rhs) {
+            ri = seen;
+        }
+        seen++;
+    }
+    if (li >= n_in || ri >= n_in || in[li].shape.rank != 2 || in[ri].shape.rank != 2) {
+        return PYC_KERNEL_WORKLOAD_ANY;
+    }
+    return classify((size_t)in[li].shape.dims[0], (size_t)in[ri].shape.dims[1], (size_t)in[li].shape.dims[1]);
+}
+
+/* ---------------------------------------------------------------- options */
+
+static pyc_compile_options default_options(void) {
+    pyc_compile_options o;
+    memset(&o, 0, sizeof(o));
+    o.enable_fusion = 1;
+    o.enable_memory_reuse = 1;
+    o.phantom_horizon_steps = 1;
+    o.objective_mode = PYC_MODE_BALANCED;
+    o.target_utilization_floor = 0.70;
+    o.deterministic_strict = 1;
+    o.cache_mode = PYC_COMPILE_CACHE_IN_MEMORY;
+    pyc_runtime_rails_default(&o.rails);
+    o.distributed.world_size = 1;
+    return o;
+}
+
+/* Out-of-range rails fall back to the defaults (reference compiler_api.c:653-690). */
+static void sanitize_rails(pyc_runtime_rails* r) {
+    pyc_runtime_rails d;
+    pyc_runtime_rails_default(&d);
+    if (r->enable_auto_switch != 0 && r->enable_auto_switch != 1) r->enable_auto_switch = d.enable_auto_switch;
+    if (r->enable_hard_rollback != 0 && r->enable_hard_rollback != 1) r->enable_hard_rollback = d.enable_hard_rollback;
+    if (r->dwell_steps == 0 || r->dwell_steps > 100000) r->dwell_steps = d.dwell_steps;
+    if (r->cooldown_steps > 100000) r->cooldown_steps = d.cooldown_steps;
+    if (r->consecutive_breach_windows == 0 || r->consecutive_breach_windows > 1000)
+        r->consecutive_breach_windows = d.consecutive_breach_windows;
+    if (r->latency_regression_threshold <= 0.0 || r->latency_regression_threshold > 1.0)
+        r->latency_regression_threshold = d.latency_regression_threshold;
+    if (r->throughput_regression_threshold <= 0.0 || r->throughput_regression_threshold > 1.0)
+        r->throughput_regression_threshold = d.throughput_regression_threshold;
+    if (r->pressure_score_threshold <= 0.0 || r->pressure_score_threshold > 10.0)
+        r->pressure_score_threshold = d.pressure_score_threshold;
+    if (r->pressure_events_threshold == 0 || r->pressure_events_threshold > 100000)
+        r->pressure_events_threshold = d.pressure_events_threshold;
+    if (r->rematerialized_tensors_threshold == 0 || r->rematerialized_tensors_threshold > 100000)
+        r->rematerialized_tensors_threshold = d.rematerialized_tensors_threshold;
+}
+
+static void sanitize_distributed(pyc_distributed_options* d) {
+    if (d->enabled != 0 && d->enabled != 1) d->enabled = 0;
+    if (d->backend < PYC_DIST_BACKEND_NONE || d->backend > PYC_DIST_BACKEND_CUSTOM) d->backend = PYC_DIST_BACKEND_NONE;
+    if (d->strategy < PYC_DIST_STRATEGY_NONE || d->strategy > PYC_DIST_STRATEGY_3D) d->strategy = PYC_DIST_STRATEGY_NONE;
+    if (d->world_size <= 0) d->world_size = 1;
+    if (d->rank < 0 || d->rank >= d->world_size) d->rank = 0;
+    if (d->local_rank < 0) d->local_rank = 0;
+    if (!d->enabled) {
+        d->backend = PYC_DIST_BACKEND_NONE;
+        d->strategy = PYC_DIST_STRATEGY_NONE;
+        d->world_size = 1;
+        d->rank = 0;
+        d->local_rank = 0;
+        d->backend_path = NULL;
+        d->config_json = NULL;
+    }
+}
+
+static uint64_t mix(uint64_t key, uint64_t v) {
+    const uint64_t x = key ^ v;
+    return fnv1a(FNV_BASIS, &x, sizeof(x));
+}
+
+static uint64_t cache_key_of(uint64_t fp, pyc_backend backend, const pyc_compile_options* o) {
+    uint64_t k = fp;
+    const uint64_t fields[] = {
+        (uint64_t)backend, (uint64_t)o->enable_fusion, (uint64_t)o->enable_memory_reuse,
+        (uint64_t)o->enable_autotune, (uint64_t)o->enable_speculative_plans, (uint64_t)o->enable_phantom_graph,
+        (uint64_t)o->max_speculative_plans, (uint64_t)o->phantom_horizon_steps, (uint64_t)o->objective_mode,
+        (uint64_t)o->memory_budget_bytes, (uint64_t)(o->target_utilization_floor * 1000.0),
+        (uint64_t)o->deterministic_strict, (uint64_t)o->cache_mode, (uint64_t)(o->compile_budget_ms * 1000.0),
+        (uint64_t)o->distributed.enabled, (uint64_t)o->distributed.backend, (uint64_t)o->distributed.strategy,
+        (uint64_t)o->distributed.world_size, (uint64_t)o->distributed.rank, (uint64_t)o->distributed.local_rank};
+    size_t i;
+    for (i = 0; i < sizeof(fields) / sizeof(fields[0]); ++i) {
+        k = mix(k, fields[i]);
+    }
+    if (o->autotune_db_path && o->autotune_db_path[0]) {
+        k ^= fnv1a(FNV_BASIS, o->autotune_db_path, strlen(o->autotune_db_path));
+    }
+    if (o->distributed.backend_path && o->distributed.backend_path[0]) {
+        k ^= fnv1a(FNV_BASIS, o->distributed.backend_path, strlen(o->distributed.backend_path));
+    }
+    if (o->distributed.config_json && o->distributed.config_json[0]) {
+        k ^= fnv1a(FNV_BASIS, o->distributed.config_json, strlen(o->distributed.config_json));
+    }
+    return k;
+}
+
+/* ---------------------------------------------------------------- compile cache */
+
+typedef struct {
+    int valid;
+    uint64_t key;
+    compiled_artifacts* art;
+} cache_slot;
+
+static cache_slot g_cache[CACHE_MAX];
+static size_t g_cache_next;
+static pyc_mutex g_cache_lock = PYC_MUTEX_INIT;
+
+static int cache_lookup(uint64_t key, compiled_artifacts* out) {
+    size_t i;
+    int hit = 0;
+    pyc_mutex_lock(&g_cache_lock);
+    for (i = 0; i < CACHE_MAX && !hit; ++i) {
+        if (g_cache[i].valid && g_cache[i].key == key) {
+            *out = *g_cache[i].art;
+            hit = 1;
+        }
+    }
+    pyc_mutex_unlock(&g_cache_lock);
+    return hit;
+}
+
+static void cache_store(uint64_t key, const compiled_artifacts* art) {
+    cache_slot* s;
+    compiled_artifacts* copy = (compiled_artifacts*)malloc(sizeof(*copy));
+    if (!copy) {
+        return;
+    }
+    *copy = *art;
+    pyc_mutex_lock(&g_cache_lock);
+    s = &g_cache[g_cache_next++ % CACHE_MAX];
+    free(s->art);
+    s->valid = 1;
+    s->key = key;
+    s->art = copy;
+    pyc_mutex_unlock(&g_cache_lock);
+}
+
+/* ---------------------------------------------------------------- kernel catalog / plans */
+
+/* The two generic "matmul_fused" candidates every backend starts with
+ * (reference compiler_api.c:2094-2122). */
+static void ensure_catalog(pyc_backend backend) {
+    pyc_kernel_desc probe, d;
+    const int gpu = backend == PYC_BACKEND_CUDA;
+    if (pyc_kernel_select("matmul_fused", backend, &probe) == 0) {
+        return;
+    }
+    memset(&d, 0, sizeof(d));
+    strcpy(d.op_key, "matmul_fused");
+    d.backend = backend;
+    strcpy(d.symbol, gpu ? "matmul_cuda_ref" : "matmul_cpu_ref");
+    d.priority = 1;
+    d.estimated_occupancy = 0.55;
+    d.tensor_core_eligible = gpu;
+    d.shared_mem_bytes = 8 * 1024;
+    d.reg_pressure_class = 2;
+    (void)pyc_kernel_register(&d);
+    strcpy(d.symbol, gpu ? "matmul_cuda_tuned" : "matmul_cpu_tuned");
+    d.priority = 2;
+    d.estimated_occupancy = 0.75;
+    d.shared_mem_bytes = 16 * 1024;
+    d.reg_pressure_class = 3;
+    (void)pyc_kernel_register(&d);
+}
+
+static pyc_kernel_hardware_family hw_family(pyc_backend backend) {
+    return backend == PYC_BACKEND_CUDA ? pyc_cuda_current_hardware_family() : PYC_KERNEL_HARDWARE_GENERIC;
+}
+
+static void context_from_stats(const pyc_alloc_stats* s, size_t budget, pyc_kernel_workload_family wl,
+                               pyc_kernel_hardware_family hw, pyc_kernel_coselect_context* ctx) {
+    memset(ctx, 0, sizeof(*ctx));
+    ctx->pressure_score = s->pressure_score;
+    ctx->pressure_events = s->pressure_events;
+    ctx->rematerialized_tensors = s->rematerialized_tensors;
+    ctx->reused_allocations = s->reused_allocations;
+    ctx->total_requested_bytes = s->total_requested_bytes;
+    ctx->peak_bytes = s->peak_bytes;
+    ctx->memory_budget_bytes = budget;
+    ctx->workload_family = wl;
+    ctx->hardware_family = hw;
+}
+
+/* One plan: lifetime [i, i+2] per value, 64-byte alignment, then an
+ * allocator-aware co-selection of the "matmul_fused" kernel
+ * (reference compiler_api.c:1374-1519). */
+static int build_plan_variant(const pyc_ir_module* m, pyc_backend backend, const pyc_compile_options* o,
+                              pyc_objective_mode mode, const char* bucket, const char* sig, double conf,
+                              spec_plan* out) {
+    size_t i;
+    pyc_alloc_stats st;
+    pyc_kernel_coselect_context ctx;
+    memset(out, 0, sizeof(*out));
+    out->module = *m;
+    pyc_alloc_plan_init(&out->alloc_plan);
+    for (i = 0; i < m->op_count; ++i) {
+        const pyc_ir_op* op = &m->ops[i];
+        pyc_alloc_request r;
+        const size_t bytes = shape_elems(&op->shape) * dtype_bytes(op->dtype);
+        if (bytes == 0) {
+            continue;
+        }
+        r.tensor_id = (int)i;
+        r.size_bytes = bytes;
+        r.alignment = 64;
+        r.start_step = (int)i;
+        r.end_step = (int)i + 2;
+        if (pyc_alloc_plan_add_request(&out->alloc_plan, r) != 0) {
+            return -1;
+        }
+    }
+    if (pyc_alloc_plan_build_with_mode(&out->alloc_plan, mode, o->memory_budget_bytes) != 0) {
+        return -1;
+    }
+    pyc_alloc_plan_stats(&out->alloc_plan, &st);
+    context_from_stats(&st, o->memory_budget_bytes, module_workload(m, NULL, 0), hw_family(backend), &ctx);
+    out->has_selected =
+        pyc_kernel_coselect_with_context("matmul_fused", backend, mode, &ctx, &out->selected, &out->trace) == 0;
+    out->mode = mode;
+    out->confidence = conf;
+    copy_str(out->bucket, sizeof(out->bucket), bucket);
+    copy_str(out->signature, sizeof(out->signature), sig);
+    out->valid = 1;
+    return 0;
+}
+
+/* Input-scaled copy of the module (every INPUT dim times `scale`), shapes re-inferred. */
+static int scaled_module(const pyc_ir_module* base, size_t scale, pyc_ir_module* out) {
+    pyc_pass_pipeline p;
+    pyc_pass_report rep;
+    size_t i, d;
+    *out = *base;
+    if (scale == 1) {
+        return 0;
+    }
+    for (i = 0; i < out->op_count; ++i) {
+        if (out->ops[i].kind != PYC_IR_OP_INPUT) {
+            continue;
+        }
+        for (d = 0; d < out->ops[i].shape.rank; ++d) {
+            if (out->ops[i].shape.dims[d] > INT64_MAX / (int64_t)scale) {
+                return -1;
+            }
+            out->ops[i].shape.dims[d] *= (int64_t)scale;
+        }
+    }
+    memset(&p, 0, sizeof(p));
+    p.config.shape_inference = 1;
+    return pyc_pass_pipeline_run(&p, out, &rep) == 0 && rep.errors == 0 ? 0 : -1;
+}
+
+static void apply_plan(pyc_compiled_model* model, const spec_plan* sp) {
+    if (!sp || !sp->valid) {
+        return;
+    }
+    model->art.alloc_plan = sp->alloc_plan;
+    model->art.trace = sp->trace;
+    model->art.has_selected = sp->has_selected;
+    if (sp->has_selected) {
+        model->art.selected = sp->selected;
+    } else {
+        memset(&model->art.selected, 0, sizeof(model->art.selected));
+    }
+    model->art.spec_confidence = sp->confidence;
+    copy_str(model->art.spec_bucket, sizeof(model->art.spec_bucket), sp->bucket);
+    copy_str(model->art.spec_signature, sizeof(model->art.spec_signature), sp->signature);
+}
+
+/* Lookup order: signature+mode, signature, bucket+mode, bucket
+ * (reference compiler_api.c:1547-1599). */
+static const spec_plan* find_plan(const pyc_compiled_model* model, pyc_objective_mode mode, const char* sig,
+                                  const char* bucket) {
+    int pass;
+    size_t i;
+    for (pass = 0; pass < 4; ++pass) {
+        const int by_sig = pass < 2;
+        const int want_mode = (pass % 2) == 0;
+        const char* key = by_sig ? sig : bucket;
+        if (!key || !key[0]) {
+            continue;
+        }
+        for (i = 0; i < model->art.spec_count; ++i) {
+            const spec_plan* sp = &model->art.spec[i];
+            if (!sp->valid || (want_mode && sp->mode != mode)) {
+                continue;
+            }
+            if (strcmp(by_sig ? sp->signature : sp->bucket, key) == 0) {
+                return sp;
+            }
+        }
+    }
+    return NULL;
+}
+
+static int init_spec_plans(pyc_compiled_model* model, const pyc_pass_report* rep) {
+    static const size_t scales[SPEC_MAX] = {1, 2, 4};
+    compiled_artifacts* a = &model->art;
+    size_t want, i;
+    a->spec_count = 0;
+    module_bucket(&a->module, a->spec_bucket, sizeof(a->spec_bucket), a->spec_signature, sizeof(a->spec_signature));
+    a->spec_confidence = rep->speculative_confidence;
+    if (!model->options.enable_speculative_plans) {
+        return 0;
+    }
+    want = model->options.max_speculative_plans ? model->options.max_speculative_plans : rep->speculative_plan_count;
+    if (want == 0 || want > SPEC_MAX) {
+        want = SPEC_MAX;
+    }
+    for (i = 0; i < want; ++i) {
+        pyc_ir_module* sm = (pyc_ir_module*)malloc(sizeof(*sm));
+        char b[64], s[SIG_MAX];
+        double c = a->spec_confidence * (i == 0 ? 1.0 : (i == 1 ? 0.95 : 0.85));
+        int rc;
+        if (!sm) {
+            return -1;
+        }
+        if (scaled_module(&a->module, scales[i], sm) != 0) {
+            free(sm);
+            return -1;
+        }
+        module_bucket(sm, b, sizeof(b), s, sizeof(s));
+        rc = build_plan_variant(sm, model->backend, &model->options, model->options.objective_mode, b, s, c,
+                                &a->spec[a->spec_count]);
+        free(sm);
+        if (rc != 0) {
+            return -1;
+        }
+        a->spec_count++;
+    }
+    if (a->spec_count > 0) {
+        apply_plan(model, &a->spec[0]);
+    }
+    return 0;
+}
+
+/* ---------------------------------------------------------------- phantom graph */
+
+static void phantom_init(pyc_compiled_model* model, const pyc_pass_report* rep) {
+    phantom_state* ph = &model->art.phantom;
+    memset(ph, 0, sizeof(*ph));
+    if (!model->options.enable_phantom_graph) {
+        return;
+    }
+    ph->enabled = 1;
+    ph->horizon = model->options.phantom_horizon_steps ? model->options.phantom_horizon_steps : 1;
+    ph->confidence = rep->phantom_confidence;
+    copy_str(ph->exp_bucket, sizeof(ph->exp_bucket), rep->phantom_shape_bucket);
+    copy_str(ph->exp_sig, sizeof(ph->exp_sig), rep->phantom_shape_signature);
+}
+
+static double phantom_score(const phantom_state* ph) {
+    if (ph->exp_sig[0] && ph->obs_sig[0] && strcmp(ph->exp_sig, ph->obs_sig) == 0) {
+        return 1.0;
+    }
+    if (ph->exp_bucket[0] && ph->obs_bucket[0] && strcmp(ph->exp_bucket, ph->obs_bucket) == 0) {
+        return 0.75;
+    }
+    return (ph->exp_sig[0] || ph->obs_sig[0]) ? 0.25 : 0.0;
+}
+
+static int phantom_compare(phantom_state* ph, const char* bucket, const char* sig, double* score) {
+    int hit;
+    *score = 0.0;
+    if (!ph->enabled) {
+        return 0;
+    }
+    copy_str(ph->obs_bucket, sizeof(ph->obs_bucket), bucket);
+    copy_str(ph->obs_sig, sizeof(ph->obs_sig), sig);
+    *score = ph->last_score = phantom_score(ph);
+    hit = *score >= 0.999;
+    if (hit) {
+        ph->matches++;
+    } else {
+        ph->mismatches++;
+    }
+    return hit;
+}
+
+/* After a run: confidence follows the match score; a persistent change of
+ * shape (every `horizon` mismatches) re-targets the expectation. */
+static void phantom_adapt(phantom_state* ph, const char* bucket, const char* sig, int error) {
+    const int differs = (sig && sig[0] && strcmp(ph->exp_sig, sig) != 0) ||
+                        (bucket && bucket[0] && strcmp(ph->exp_bucket, bucket) != 0);
+    if (!ph->enabled || error) {
+        return;
+    }
+    if (!differs) {
+        ph->confidence = 0.85 * ph->confidence + 0.15 * ph->last_score;
+        return;
+    }
+    if (ph->horizon > 1 && ph->mismatches % ph->horizon != 0) {
+        ph->confidence = 0.7 * ph->confidence + 0.3 * ph->last_score;
+        return;
+    }
+    ph->reshapes++;
+    if (bucket && bucket[0]) {
+        copy_str(ph->exp_bucket, sizeof(ph->exp_bucket), bucket);
+    }
+    if (sig && sig[0]) {
+        copy_str(ph->exp_sig, sizeof(ph->exp_sig), sig);
+    }
+    ph->confidence = 0.6 * ph->confidence + 0.4 * ph->last_score;
+}
+
+/* ---------------------------------------------------------------- autotune DB */
+
+static void autotune_path(const pyc_compile_options* o, char* out, size_t cap) {
+    const char* env = getenv("PYC_AUTOTUNE_DB_PATH");
+    if (o->autotune_db_path && o->autotune_db_path[0]) {
+        copy_str(out, cap, o->autotune_db_path);
+    } else if (env && env[0]) {
+        copy_str(out, cap, env);
+    } else {
+        copy_str(out, cap, "pyc_autotune.db");
+    }
+}
+
+typedef struct {
+    char op[PYC_KERNEL_OP_KEY_MAX];
+    int backend;
+    char symbol[PYC_KERNEL_SYMBOL_MAX];
+    double ms;
+} db_row;
+
+/* "op|backend|symbol|best_ms" (reference compiler_api.c:2155-2172). */
+static int parse_row(const char* line, db_row* r) {
+    return sscanf(line, "%63[^|]|%d|%127[^|]|%lf", r->op, &r->backend, r->symbol, &r->ms) == 4 && r->ms > 0.0 ? 0 : -1;
+}
+
+static int autotune_load(const char* path, const char* op, pyc_backend backend) {
+    FILE* f;
+    char line[512];
+    int loaded = 0;
+    if (!path[0] || !(f = fopen(path, "r"))) {
+        return 0;
+    }
+    while (fgets(line, sizeof(line), f)) {
+        db_row r;
+        if (parse_row(line, &r) == 0 && strcmp(r.op, op) == 0 && r.backend == (int)backend &&
+            pyc_kernel_benchmark_update_symbol(op, backend, r.symbol, r.ms) == 0) {
+            loaded = 1;
+        }
+    }
+    fclose(f);
+    return loaded;
+}
+
+/* Append the record, then rewrite the file keeping the best time per
+ * (op, backend, symbol); both under an exclusive flock on "<db>.lock". */
+static int autotune_persist(const char* path, const char* op, pyc_backend backend, const char* sym, double ms) {
+    char lock_path[600];
+    int fd, rc = -1;
+    FILE* f;
+    if (!path[0] || !sym || ms <= 0.0) {
+        return -1;
+    }
+    snprintf(lock_path, sizeof(lock_path), "%s.lock", path);
+    fd = open(lock_path, O_CREAT | O_RDWR, 0644);
+    if (fd < 0) {
+        return -1;
+    }
+    if (flock(fd, LOCK_EX) != 0) {
+        close(fd);
+        return -1;
+    }
+    f = fopen(path, "a");
+    if (f && fprintf(f, "%s|%d|%s|%.6f\n", op, (int)backend, sym, ms) > 0 && fclose(f) == 0) {
+        db_row* rows = (db_row*)calloc(1024, sizeof(db_row));
+        size_t n = 0, i;
+        char line[512];
+        f = rows ? fopen(path, "r") : NULL;
+        if (f) {
+            while (fgets(line, sizeof(line), f)) {
+                db_row r;
+                int merged = 0;
+                if (parse_row(line, &r) != 0) {
+                    continue;
+                }
+                for (i = 0; i < n && !merged; ++i) {
+                    if (strcmp(rows[i].op, r.op) == 0 && rows[i].backend == r.backend &&
+                        strcmp(rows[i].symbol, r.symbol) == 0) {
+                        if (r.ms < rows[i].ms) {
+                            rows[i].ms = r.ms;
+                        }
+                        merged = 1;
+                    }
+                }
+                if (!merged && n < 1024) {
+                    rows[n++] = r;
+                }
+            }
+            fclose(f);
+            f = fopen(path, "w");
+            if (f) {
+                rc = 0;
+                for (i = 0; i < n; ++i) {
+                    if (fprintf(f, "%s|%d|%s|%.6f\n", rows[i].op, rows[i].backend, rows[i].symbol, rows[i].ms) < 0) {
+                        rc = -1;
+                    }
+                }
+                if (fclose(f) != 0) {
+                    rc = -1;
+                }
+            }
+        }
+        free(rows);
+    } else if (f) {
+        fclose(f);
+    }
+    flock(fd, LOCK_UN);
+    close(fd);
+    return rc;
+}
+
+/* Heuristic time of a not-measured candidate (reference compiler_api.c:562-589);
+ * used only on the CPU backend, where no device timing exists. */
+static double estimate_ms(double base, const pyc_kernel_desc* c, pyc_objective_mode mode, double pressure) {
+    double adj = base * (1.0 + (1.0 - c->estimated_occupancy) * 0.08 +
+                         (pressure > 0.0 ? (double)c->reg_pressure_class * pressure * 0.005 : 0.0) +
+                         (mode == PYC_MODE_MEMORY_FIRST ? (double)c->shared_mem_bytes / 131072.0 : 0.0));
+    if (c->tensor_core_eligible) {
+        adj *= 0.97;
+    }
+    return adj > 0.0 ? adj : 0.001;
+}
+
+/* ---------------------------------------------------------------- CPU executor */
+
+typedef struct {
+    const float* a;
+    const float* b;
+    float* c;
+    size_t k, n, r0, r1;
+} rows_job;
+
+/* C = A B in fp32: rows zeroed, then k ascending with c += a*b per step,
+ * matching the reference executor's order (compiler_api.c:1747-1781). */
+static void gemm_rows(const rows_job* j) {
+    size_t r, kk, col;
+    for (r = j->r0; r < j->r1; ++r) {
+        float* c = j->c + r * j->n;
+        memset(c, 0, j->n * sizeof(float));
+        for (kk = 0; kk < j->k; ++kk) {
+            const float av = j->a[r * j->k + kk];
+            const float* b = j->b + kk * j->n;
+            for (col = 0; col < j->n; ++col) {
+                c[col] += av * b[col];
+            }
+        }
+    }
+}
+
+static void* gemm_rows_thread(void* p) {
+    gemm_rows((const rows_job*)p);
+    return NULL;
+}
+
+static void cpu_gemm(const float* a, const float* b, float* c, size_t m, size_t k, size_t n) {
+    const char* env = getenv("PYC_NUM_THREADS");
+    long want = env && env[0] ? strtol(env, NULL, 10) : 1;
+    size_t t, nt = want > 0 ? (size_t)want : 1, per;
+    pthread_t tid[32];
+    rows_job jobs[32];
+    int started[32];
+    if (nt > 32) nt = 32;
+    if (nt > m) nt = m;
+    if (m < 8) nt = 1;
+    if (nt <= 1) {
+        rows_job one = {a, b, c, k, n, 0, m};
+        gemm_rows(&one);
+        return;
+    }
+    per = (m + nt - 1) / nt;
+    for (t = 0; t < nt; ++t) {
+        rows_job j = {a, b, c, k, n, t * per < m ? t * per : m, (t + 1) * per < m ? (t + 1) * per : m};
+        jobs[t] = j;
+        started[t] = pthread_create(&tid[t], NULL, gemm_rows_thread, &jobs[t]) == 0;
+        if (!started[t]) {
+            gemm_rows(&jobs[t]);
+        }
+    }
+    for (t = 0; t < nt; ++t) {
+        if (started[t]) {
+            pthread_join(tid[t], NULL);
+        }
+    }
+}
+
+/* The engine's CPU executor: F32 INPUT/MATMUL/ADD/RELU/OUTPUT (reference
+ * compiler_api.c:1877-2092), with ADD broadcasting a [N] or [1] operand. */
+static int execute_cpu_graph(const pyc_ir_module* m, const pyc_tensor* inputs, size_t n_in, pyc_tensor* outputs,
+                             size_t n_out, void* ctx) {
+    pyc_compiled_model* model = (pyc_compiled_model*)ctx;
+    const float** val = (const float**)calloc(m->op_count, sizeof(float*));
+    float** owned = (float**)calloc(m->op_count, sizeof(float*));
+    size_t* count = (size_t*)calloc(m->op_count, sizeof(size_t));
+    size_t i, ii = 0, oi = 0;
+    int fail = 0;
+    if (!val || !owned || !count) {
+        free(val);
+        free(owned);
+        free(count);
+        return -1;
+    }
+    for (i = 0; i < m->op_count && !fail; ++i) {
+        const pyc_ir_op* op = &m->ops[i];
+        const int a = op->input_count > 0 ? op->input_ids[0] : -1;
+        const int b = op->input_count > 1 ? op->input_ids[1] : -1;
+        float* out = NULL;
+        size_t need = 0;
+        switch (op->kind) {
+            case PYC_IR_OP_INPUT:
+                count[i] = shape_elems(&op->shape);
+                if (ii >= n_in || !inputs[ii].data || inputs[ii].dtype != PYC_DTYPE_F32 || count[i] == 0 ||
+                    inputs[ii].size_bytes < count[i] * sizeof(float)) {
+                    fail = 1;
+                    break;
+                }
+                val[i] = (const float*)inputs[ii++].data;
+                continue;
+            case PYC_IR_OP_MATMUL:
+                if (a < 0 || b < 0 || !val[a] || !val[b] || m->ops[a].shape.rank != 2 || m->ops[b].shape.rank != 2 ||
+                    m->ops[a].shape.dims[1] != m->ops[b].shape.dims[0]) {
+                    fail = 1;
+                    break;
+                }
+                count[i] = (size_t)m->ops[a].shape.dims[0] * (size_t)m->ops[b].shape.dims[1];
+                break;
+            case PYC_IR_OP_ADD:
+                if (a < 0 || b < 0 || !val[a] || !val[b] || count[b] == 0 || count[a] % count[b] != 0) {
+                    fail = 1;
+                    break;
+                }
+                count[i] = count[a];
+                break;
+            case PYC_IR_OP_RELU:
+                if (a < 0 || !val[a]) {
+                    fail = 1;
+                    break;
+                }
+                count[i] = count[a];
+                break;
+            case PYC_IR_OP_OUTPUT:
+                if (a < 0 || !val[a] || oi >= n_out || !outputs[oi].data ||
+                    outputs[oi].size_bytes < count[a] * sizeof(float)) {
+                    fail = 1;
+                    break;
+                }
+                memcpy(outputs[oi++].data, val[a], count[a] * sizeof(float));
+                continue;
+            default:
+                fail = 1; /* CONST / GELU / REDUCE_SUM / LAYERNORM / CONV2D / ATTENTION */
+                break;
+        }
+        if (fail) {
+            break;
+        }
+        need = count[i] * sizeof(float);
+        if (model && model->workspace[i] && model->workspace_bytes[i] >= need) {
+            out = model->workspace[i];
+        } else {
+            out = owned[i] = (float*)malloc(need ? need : 1);
+            if (!out) {
+                fail = 1;
+                break;
+            }
+        }
+        if (op->kind == PYC_IR_OP_MATMUL) {
+            cpu_gemm(val[a], val[b], out, (size_t)m->ops[a].shape.dims[0], (size_t)m->ops[a].shape.dims[1],
+                     (size_t)m->ops[b].shape.dims[1]);
+        } else if (op->kind == PYC_IR_OP_ADD) {
+            size_t j;
+            const size_t nb = count[b];
+            for (j = 0; j < count[i]; ++j) {
+                out[j] = val[a][j] + val[b][j % nb];
+            }
+        } else {
+            size_t j;
+            for (j = 0; j < count[i]; ++j) {
+                out[j] = val[a][j] > 0.0f ? val[a][j] : 0.0f;
+            }
+        }
+        val[i] = out;
+    }
+    for (i = 0; i < m->op_count; ++i) {
+        free(owned[i]);
+    }
+    free(val);
+    free(owned);
+    free(count);
+    return fail ? -1 : 0;
+}
+
+static void release_workspace(pyc_compiled_model* model) {
+    size_t i;
+    for (i = 0; i < PYC_IR_MAX_OPS; ++i) {
+        free(model->workspace[i]);
+        model->workspace[i] = NULL;
+        model->workspace_bytes[i] = 0;
+    }
+}
+
+/* Preallocated fp32 buffers for the CPU executor's MATMUL/ADD/RELU values. */
+static int init_workspace(pyc_compiled_model* model) {
+    size_t i;
+    if (model->backend != PYC_BACKEND_CPU && model->backend != PYC_BACKEND_CUDA) {
+        return 0;
+    }
+    for (i = 0; i < model->art.module.op_count; ++i) {
+        const pyc_ir_op* op = &model->art.module.ops[i];
+        const size_t e = shape_elems(&op->shape);
+        if ((op->kind != PYC_IR_OP_MATMUL && op->kind != PYC_IR_OP_ADD && op->kind != PYC_IR_OP_RELU) || e == 0 ||
+            op->dtype != PYC_DTYPE_F32) {
+            continue;
+        }
+        model->workspace[i] = (float*)malloc(e * sizeof(float));
+        if (!model->workspace[i]) {
+            release_workspace(model);
+            return -1;
+        }
+        model->workspace_bytes[i] = e * sizeof(float);
+    }
+    return 0;
+}
+
+/* ---------------------------------------------------------------- compile */
+
+static void compile_log(pyc_compiled_model* model) {
+    const compiled_artifacts* a = &model->art;
+    const pyc_pass_report* r = &a->report;
+    logbuf lb = {model->log, sizeof(model->log), 0};
+    model->log[0] = '\0';
+    logf_(&lb, "mode=%d budget=%zu pressure=%.6f kernel=%s score=%.3f util=%.3f alloc_penalty=%.3f "
+               "reuse_bonus=%.3f kernel_candidates=%zu det=%d cache_hit=%d compile_ms=%.3f budget_ms=%.3f "
+               "budget_exceeded=%d graph_breaks=%zu break_first=%s@%d break_counts=%zu,%zu,%zu,%zu,%zu "
+               "compilability=%.3f autotune_loaded=%d spec_plans=%zu spec_bucket=%s spec_conf=%.3f",
+          (int)model->options.objective_mode, model->options.memory_budget_bytes, a->alloc_plan.pressure_score,
+          a->has_selected ? a->selected.symbol : "none", a->trace.selected_score,
+          a->trace.selected_estimated_utilization, a->trace.allocator_penalty, a->trace.reuse_bonus,
+          a->trace.candidates_considered, model->options.deterministic_strict ? 1 : 0, model->cache_hit,
+          model->compile_ms, model->options.compile_budget_ms, model->budget_exceeded, r->graph_break_count,
+          r->first_graph_break_op_name, r->first_graph_break_op_id, r->graph_break_const_count,
+          r->graph_break_gelu_count, r->graph_break_reduce_sum_count, r->graph_break_layernorm_count,
+          r->graph_break_unknown_count, r->compilability_score, model->autotune_loaded, a->spec_count,
+          a->spec_bucket, a->spec_confidence);
+}
+
+pyc_status pyc_compile_model(const pyc_model_desc* desc, const pyc_compile_options* options,
+                             pyc_compiled_model** out_model) {
+    pyc_ir_diagnostic diag;
+    pyc_compiled_model* model;
+    uint64_t source_fp = 0;
+    double t0;
+    const char* delay;
+    if (!desc || !desc->module || !out_model) {
+        return PYC_STATUS_INVALID_ARGUMENT;
+    }
+    if (pyc_ir_verify(desc->module, &diag) != 0) {
+        return PYC_STATUS_VERIFY_FAILED;
+    }
+    model = (pyc_compiled_model*)calloc(1, sizeof(*model));
+    if (!model) {
+        return PYC_STATUS_COMPILE_FAILED;
+    }
+    model->art.module = *desc->module;
+    model->backend = desc->backend;
+    model->options = default_options();
+    if (options) {
+        model->options = *options;
+    }
+    {
+        pyc_compile_options* o = &model->options;
+        if (o->cache_mode != PYC_COMPILE_CACHE_DISABLED && o->cache_mode != PYC_COMPILE_CACHE_IN_MEMORY) {
+            o->cache_mode = PYC_COMPILE_CACHE_IN_MEMORY;
+        }
+        if (o->enable_speculative_plans != 0 && o->enable_speculative_plans != 1) o->enable_speculative_plans = 0;
+        if (o->enable_phantom_graph != 0 && o->enable_phantom_graph != 1) o->enable_phantom_graph = 0;
+        if (o->max_speculative_plans > SPEC_MAX) o->max_speculative_plans = SPEC_MAX;
+        if (o->phantom_horizon_steps == 0) o->phantom_horizon_steps = 1;
+        if (o->compile_budget_ms < 0.0) o->compile_budget_ms = 0.0;
+        if (o->deterministic_strict) {
+            o->rails.enable_auto_switch = 0;
+            o->rails.enable_hard_rollback = 0;
+            model->contract_enforced = 1;
+        }
+        sanitize_rails(&o->rails);
+        sanitize_distributed(&o->distributed);
+        if (o->objective_mode < PYC_MODE_BALANCED || o->objective_mode > PYC_MODE_UTILIZATION_FIRST) {
+            o->objective_mode = PYC_MODE_BALANCED;
+        }
+        if (o->distributed.enabled && (!o->distributed.backend_path || !o->distributed.backend_path[0])) {
+            free(model);
+            return PYC_STATUS_INVALID_ARGUMENT;
+        }
+    }
+    autotune_path(&model->options, model->autotune_db, sizeof(model->autotune_db));
+    pyc_runtime_controller_init(&model->controller, model->options.objective_mode);
+    pyc_cuda_dispatch_trace_init(&model->trace);
+    if (model->backend == PYC_BACKEND_CUDA) {
+        pyc_cutlass_registry_init();
+    }
+    if (module_fingerprint(desc->module, &source_fp) != 0) {
+        free(model);
+        return PYC_STATUS_COMPILE_FAILED;
+    }
+    model->cache_key = cache_key_of(source_fp, model->backend, &model->options);
+    t0 = now_ms();
+    if (model->options.cache_mode == PYC_COMPILE_CACHE_IN_MEMORY && cache_lookup(model->cache_key, &model->art)) {
+        model->cache_hit = 1;
+    } else {
+        pyc_pass_pipeline pipe;
+        delay = getenv("PYC_COMPILE_DELAY_MS");
+        if (delay && strtol(delay, NULL, 10) > 0) {
+            const long ms = strtol(delay, NULL, 10);
+            struct timespec ts = {ms / 1000, (ms % 1000) * 1000000L};
+            nanosleep(&ts, NULL);
+        }
+        pyc_pass_pipeline_default(&pipe);
+        pipe.config.fusion = 0; /* executed modules keep their ADD/activation ops */
+        if (pyc_pass_pipeline_run(&pipe, &model->art.module, &model->art.report) != 0 || model->art.report.errors) {
+            free(model);
+            return PYC_STATUS_COMPILE_FAILED;
+        }
+        if (module_fingerprint(&model->art.module, &model->art.fingerprint) != 0) {
+            free(model);
+            return PYC_STATUS_COMPILE_FAILED;
+        }
+        ensure_catalog(model->backend);
+        if (model->options.enable_autotune) {
+            model->autotune_loaded = autotune_load(model->autotune_db, "matmul_fused", model->backend);
+        }
+        if (init_spec_plans(model, &model->art.report) != 0) {
+            free(model);
+            return PYC_STATUS_COMPILE_FAILED;
+        }
+        phantom_init(model, &model->art.report);
+        if (model->art.spec_count == 0) {
+            spec_plan* base = (spec_plan*)malloc(sizeof(*base));
+            if (!base || build_plan_variant(&model->art.module, model->backend, &model->options,
+                                            model->options.objective_mode, model->art.spec_bucket,
+                                            model->art.spec_signature, model->art.report.speculative_confidence,
+                                            base) != 0) {
+                free(base);
+                free(model);
+                return PYC_STATUS_COMPILE_FAILED;
+            }
+            apply_plan(model, base);
+            free(base);
+        }
+        if (model->options.cache_mode == PYC_COMPILE_CACHE_IN_MEMORY) {
+            cache_store(model->cache_key, &model->art);
+        }
+    }
+    model->candidate_count = pyc_kernel_collect("matmul_fused", model->backend, model->candidates, CANDIDATE_MAX);
+    if (init_workspace(model) != 0) {
+        free(model);
+        return PYC_STATUS_COMPILE_FAILED;
+    }
+    model->compile_ms = now_ms() - t0;
+    model->budget_exceeded = model->options.compile_budget_ms > 0.0 && model->compile_ms > model->options.compile_budget_ms;
+    compile_log(model);
+    *out_model = model;
+    return PYC_STATUS_OK;
+}
+
+/* ---------------------------------------------------------------- run */
+
+static void run_log(pyc_compiled_model* model, const pyc_alloc_stats* st, pyc_kernel_workload_family wl,
+                    pyc_kernel_hardware_family hw, int contract_ok, const char* contract_why, int spec_hit,
+                    int phantom_hit, const char* bucket) {
+    const compiled_artifacts* a = &model->art;
+    const pyc_pass_report* r = &a->report;
+    const phantom_state* ph = &a->phantom;
+    logbuf lb = {model->log, sizeof(model->log), 0};
+    model->log[0] = '\0';
+    if (!env_on_default("PYC_ENABLE_RUNTIME_DECISION_LOG")) {
+        return;
+    }
+    logf_(&lb, "mode=%d shadow_mode=%d shadow_reason=%d rollback=%d rollback_count=%zu pressure=%.6f kernel=%s "
+               "score=%.3f util=%.3f alloc_penalty=%.3f reuse_bonus=%.3f kernel_candidates=%zu workload=%s hw=%s ",
+          (int)model->options.objective_mode, (int)model->controller.recommended_mode,
+          (int)model->controller.recommendation_reason, (int)model->controller.last_rollback_reason,
+          model->controller.rollback_count, st->pressure_score, a->has_selected ? a->selected.symbol : "none",
+          a->trace.selected_score, a->trace.selected_estimated_utilization, a->trace.allocator_penalty,
+          a->trace.reuse_bonus, a->trace.candidates_considered, pyc_kernel_workload_family_name(wl),
+          pyc_kernel_hardware_family_name(hw));
+    logf_(&lb, "cuda_fallback=%d cuda_reason=%s contract=%d contract_reason=%s guard_miss=%zu fallback=%zu "
+               "cache_hit=%d budget_exceeded=%d graph_breaks=%zu break_first=%s@%d break_counts=%zu,%zu,%zu,%zu,%zu "
+               "compilability=%.3f ",
+          model->trace.fallback_to_cpu, model->trace.reason, contract_ok, contract_why, model->guard_misses,
+          model->fallbacks, model->cache_hit, model->budget_exceeded, r->graph_break_count,
+          r->first_graph_break_op_name, r->first_graph_break_op_id, r->graph_break_const_count,
+          r->graph_break_gelu_count, r->graph_break_reduce_sum_count, r->graph_break_layernorm_count,
+          r->graph_break_unknown_count, r->compilability_score);
+    logf_(&lb, "autotune_loaded=%d autotune_saved=%d autotune_candidates=%zu spec_plans=%zu spec_hit=%d "
+               "spec_miss=%zu spec_guard=%zu spec_bucket=%s spec_conf=%.3f phantom_enabled=%d phantom_match=%d "
+               "phantom_score=%.3f phantom_matches=%zu phantom_misses=%zu phantom_reshapes=%zu phantom_expect=%s "
+               "phantom_observed=%s fp=%llu",
+          model->autotune_loaded, model->autotune_saved, model->candidate_count, a->spec_count, spec_hit,
+          model->spec_misses, model->spec_guard_misses, bucket, a->spec_confidence, ph->enabled, phantom_hit,
+          ph->last_score, ph->matches, ph->mismatches, ph->reshapes, ph->exp_sig, ph->obs_sig,
+          (unsigned long long)a->fingerprint);
+}
+
+pyc_status pyc_run_model(pyc_compiled_model* model, const pyc_tensor* inputs, size_t input_count,
+                         pyc_tensor* outputs, size_t output_count, pyc_run_stats* out_stats) {
+    const double t_start = now_ms();
+    char contract_why[64] = "ok";
+    char bucket[64] = "";
+    char sig[SIG_MAX] = "";
+    const pyc_ir_module* exec = NULL;
+    compiled_artifacts* a;
+    pyc_alloc_stats st;
+    pyc_kernel_workload_family wl;
+    pyc_kernel_hardware_family hw;
+    pyc_objective_mode active_mode;
+    pyc_rollback_reason rollback = PYC_ROLLBACK_NONE;
+    double dispatch_ms = 0.0, controller_ms = 0.0, select_ms = 0.0, run_ms, throughput, phantom_sc = 0.0;
+    int contract_ok = 1, error = 0, spec_hit = 0, phantom_hit, shape_cached = 0, exact_repeat = 0;
+    size_t guard_miss = 0, fallback = 0;
+    uint64_t hash = 0;
+
+    if (!model || !inputs || !outputs || input_count == 0 || output_count == 0) {
+        return PYC_STATUS_INVALID_ARGUMENT;
+    }
+    a = &model->art;
+    exec = &a->module;
+
+    /* stable-repeat fast path: identical descriptors as the previous good run */
+    if (model->last_valid && !model->options.enable_speculative_plans && !model->options.enable_phantom_graph &&
+        input_count <= PYC_IR_MAX_INPUTS && output_count <= PYC_IR_MAX_INPUTS &&
+        same_descriptors(inputs, input_count, model->last_in, model->last_in_count) &&
+        same_descriptors(outputs, output_count, model->last_out, model->last_out_count)) {
+        shape_cached = 1;
+        exact_repeat = env_on_default("PYC_ENABLE_STABLE_REPEAT_FASTPATH") && model->backend == PYC_BACKEND_CUDA &&
+                       !model->options.enable_autotune;
+        hash = model->last_hash;
+        copy_str(bucket, sizeof(bucket), model->last_bucket);
+        copy_str(sig, sizeof(sig), model->last_signature);
+    }
+    if (model->contract_enforced && !exact_repeat) {
+        uint64_t fp;
+        if (module_fingerprint(&a->module, &fp) != 0) {
+            contract_ok = 0;
+            error = 1;
+            guard_miss++;
+            copy_str(contract_why, sizeof(contract_why), "fingerprint_unavailable");
+        } else if (fp != a->fingerprint) {
+            contract_ok = 0;
+            error = 1;
+            guard_miss++;
+            copy_str(contract_why, sizeof(contract_why), "fingerprint_mismatch");
+        }
+    }
+    if (!shape_cached) {
+        runtime_bucket(inputs, input_count, bucket, sizeof(bucket), sig, sizeof(sig));
+        hash = runtime_hash(inputs, input_count);
+        if (model->last_valid && hash == model->last_hash && !model->options.enable_speculative_plans &&
+            !model->options.enable_phantom_graph) {
+            shape_cached = 1;
+        }
+    }
+    wl = module_workload(&a->module, inputs, input_count);
+    hw = hw_family(model->backend);
+    phantom_hit = phantom_compare(&a->phantom, bucket, sig, &phantom_sc);
+    if (!error && a->spec_count > 0) {
+        const spec_plan* sp = find_plan(model, model->options.objective_mode, sig, bucket);
+        if (sp) {
+            exec = &sp->module;
+            apply_plan(model, sp);
+            spec_hit = 1;
+        } else {
+            model->spec_misses++;
+        }
+    }
+    if (!error && !shape_cached && !inputs_match(exec, inputs, input_count, contract_why, sizeof(contract_why))) {
+        contract_ok = 0;
+        error = 1;
+        guard_miss++;
+        model->spec_guard_misses++;
+    }
+
+    pyc_cuda_dispatch_trace_init(&model->trace);
+    {
+        const double t0 = now_ms();
+        if (!error) {
+            if (model->backend == PYC_BACKEND_CPU) {
+                error = execute_cpu_graph(exec, inputs, input_count, outputs, output_count, model) != 0;
+            } else if (model->backend == PYC_BACKEND_CUDA) {
+                const pyc_cuda_dispatch_status ds = pyc_cuda_dispatch(exec, inputs, input_count, outputs, output_count,
+                                                                      execute_cpu_graph, model, &model->trace);
+                if (ds == PYC_CUDA_DISPATCH_ERROR) {
+                    error = 1;
+                } else if (ds == PYC_CUDA_DISPATCH_FALLBACK) {
+                    fallback++;
+                    if (env_on("PYC_HIP_STRICT")) {
+                        error = 1; /* strict mode: a CPU fallback is a failure */
+                    }
+                }
+            } else {
+                error = 1;
+            }
+        }
+        dispatch_ms = now_ms() - t0;
+    }
+    if (!error && !model->options.enable_speculative_plans && !model->options.enable_phantom_graph && hash != 0) {
+        size_t i;
+        model->last_valid = 1;
+        model->last_hash = hash;
+        copy_str(model->last_bucket, sizeof(model->last_bucket), bucket);
+        copy_str(model->last_signature, sizeof(model->last_signature), sig);
+        model->last_in_count = input_count <= PYC_IR_MAX_INPUTS ? input_count : 0;
+        model->last_out_count = output_count <= PYC_IR_MAX_INPUTS ? output_count : 0;
+        for (i = 0; i < model->last_in_count; ++i) model->last_in[i] = inputs[i];
+        for (i = 0; i < model->last_out_count; ++i) model->last_out[i] = outputs[i];
+    } else if (error) {
+        model->last_valid = 0;
+        model->last_hash = 0;
+        model->last_bucket[0] = '\0';
+        model->last_signature[0] = '\0';
+        model->last_in_count = model->last_out_count = 0;
+    }
+    phantom_adapt(&a->phantom, bucket, sig, error);
+
+    run_ms = now_ms() - t_start;
+    throughput = run_ms > 0.0 ? 1000.0 / run_ms : 0.0;
+    model->run_count++;
+    pyc_alloc_plan_stats(&a->alloc_plan, &st);
+    if (model->baseline_ms == 0.0) model->baseline_ms = run_ms;
+    if (model->baseline_throughput == 0.0) model->baseline_throughput = throughput;
+
+    if (!(exact_repeat || (shape_cached && !error && env_on_default("PYC_ENABLE_STABLE_REPEAT_FASTPATH") &&
+                           !model->options.enable_autotune && model->backend == PYC_BACKEND_CUDA))) {
+        pyc_runtime_window_metrics met;
+        pyc_kernel_coselect_context ctx;
+        double t0;
+        memset(&met, 0, sizeof(met));
+        met.baseline_p95_ms = model->baseline_ms;
+        met.observed_p95_ms = run_ms;
+        met.baseline_throughput = model->baseline_throughput;
+        met.observed_throughput = throughput;
+        met.pressure_score = st.pressure_score;
+        met.pressure_events = st.pressure_events;
+        met.rematerialized_tensors = st.rematerialized_tensors;
+        met.runtime_error = error;
+        t0 = now_ms();
+        if (pyc_runtime_controller_observe(&model->controller, &model->options.rails, &met, &active_mode, &rollback) != 0) {
+            return PYC_STATUS_RUNTIME_FAILED;
+        }
+        controller_ms = now_ms() - t0;
+        model->options.objective_mode = active_mode;
+        a->trace.selected_score = 0.0;
+        a->trace.selected_estimated_utilization = 0.0;
+        a->has_selected = 0;
+        t0 = now_ms();
+        context_from_stats(&st, model->options.memory_budget_bytes, wl, hw, &ctx);
+        {
+            const spec_plan* sp = a->spec_count > 0 ? find_plan(model, model->options.objective_mode, sig,
+                                                                 bucket[0] ? bucket : a->spec_bucket)
+                                                    : NULL;
+            if (sp) {
+                apply_plan(model, sp);
+            } else {
+                if (a->spec_count > 0) {
+                    model->spec_misses++;
+                }
+                a->has_selected = pyc_kernel_coselect_with_context("matmul_fused", model->backend,
+                                                                   model->options.objective_mode, &ctx, &a->selected,
+                                                                   &a->trace) == 0;
+            }
+        }
+        select_ms = now_ms() - t0;
+    } else {
+        rollback = model->controller.last_rollback_reason;
+    }
+    model->guard_misses += guard_miss;
+    model->fallbacks += fallback;
+
+    if (!error && model->options.enable_autotune) {
+        pyc_kernel_desc cand;
+        double ms;
+        model->candidate_count = pyc_kernel_collect("matmul_fused", model->backend, model->candidates, CANDIDATE_MAX);
+        memset(&cand, 0, sizeof(cand));
+        if (model->candidate_count > 0) {
+            cand = model->candidates[(model->run_count - 1) % model->candidate_count];
+        } else if (a->has_selected) {
+            cand = a->selected;
+        } else {
+            copy_str(cand.symbol, sizeof(cand.symbol), "matmul_cpu_ref");
+        }
+        if (model->backend == PYC_BACKEND_CUDA && model->trace.kernel_ms > 0.0 && !model->trace.fallback_to_cpu) {
+            ms = model->trace.kernel_ms; /* measured device time */
+        } else {
+            ms = estimate_ms(run_ms > 0.0 ? run_ms : (dispatch_ms > 0.0 ? dispatch_ms : 0.001), &cand,
+                             model->options.objective_mode, st.pressure_score);
+        }
+        if (pyc_kernel_benchmark_update_symbol("matmul_fused", model->backend, cand.symbol, ms) == 0 &&
+            autotune_persist(model->autotune_db, "matmul_fused", model->backend, cand.symbol, ms) == 0) {
+            model->autotune_saved = 1;
+        }
+    }
+
+    run_log(model, &st, wl, hw, contract_ok, contract_why, spec_hit, phantom_hit, bucket[0] ? bucket : a->spec_bucket);
+
+    if (out_stats) {
+        const phantom_state* ph = &a->phantom;
+        const pyc_pass_report* r = &a->report;
+        memset(out_stats, 0, sizeof(*out_stats));
+        out_stats->compile_ms = model->compile_ms;
+        out_stats->run_ms = run_ms;
+        out_stats->peak_bytes = st.peak_bytes;
+        out_stats->total_requested_bytes = st.total_requested_bytes;
+        out_stats->reused_allocations = st.reused_allocations;
+        out_stats->rematerialized_tensors = st.rematerialized_tensors;
+        out_stats->rematerialized_bytes = st.rematerialized_bytes;
+        out_stats->pressure_events = st.pressure_events;
+        out_stats->pressure_score = st.pressure_score;
+        out_stats->selected_kernel_score = a->trace.selected_score;
+        out_stats->selected_kernel_allocator_penalty = a->trace.allocator_penalty;
+        out_stats->selected_kernel_reuse_bonus = a->trace.reuse_bonus;
+        out_stats->estimated_utilization = a->trace.selected_estimated_utilization;
+        out_stats->active_mode = model->options.objective_mode;
+        out_stats->rollback_reason = rollback;
+        out_stats->rollback_count = model->controller.rollback_count;
+        out_stats->shadow_mode = model->controller.recommended_mode;
+        out_stats->shadow_reason = model->controller.recommendation_reason;
+        copy_str(out_stats->workload_family, sizeof(out_stats->workload_family), pyc_kernel_workload_family_name(wl));
+        copy_str(out_stats->hardware_family, sizeof(out_stats->hardware_family), pyc_kernel_hardware_family_name(hw));
+        out_stats->selected_kernel_count = a->has_selected ? 1 : 0;
+        out_stats->selected_kernel_candidates = a->trace.candidates_considered;
+        if (a->has_selected) {
+            copy_str(out_stats->selected_kernel_symbol, sizeof(out_stats->selected_kernel_symbol), a->selected.symbol);
+        }
+        copy_str(out_stats->execution_path, sizeof(out_stats->execution_path),
+                 model->backend == PYC_BACKEND_CPU ? "cpu" : model->trace.reason);
+        out_stats->dispatch_ms = dispatch_ms;
+        out_stats->graph_exec_ms = dispatch_ms;
+        out_stats->controller_ms = controller_ms;
+        out_stats->kernel_select_ms = select_ms;
+        out_stats->cuda_copy_in_ms = model->trace.copy_in_ms;
+        out_stats->cuda_kernel_ms = model->trace.kernel_ms;
+        out_stats->cuda_copy_out_ms = model->trace.copy_out_ms;
+        out_stats->cuda_sync_ms = model->trace.sync_ms;
+        out_stats->deterministic_contract_enforced = model->contract_enforced;
+        out_stats->deterministic_contract_ok = contract_ok;
+        out_stats->model_fingerprint = a->fingerprint;
+        copy_str(out_stats->deterministic_contract_reason, sizeof(out_stats->deterministic_contract_reason), contract_why);
+        out_stats->compile_cache_hit = model->cache_hit;
+        out_stats->compile_budget_exceeded = model->budget_exceeded;
+        out_stats->guard_miss_count = model->guard_misses;
+        out_stats->fallback_count = model->fallbacks;
+        out_stats->graph_break_count = r->graph_break_count;
+        out_stats->graph_break_const_count = r->graph_break_const_count;
+        out_stats->graph_break_gelu_count = r->graph_break_gelu_count;
+        out_stats->graph_break_reduce_sum_count = r->graph_break_reduce_sum_count;
+        out_stats->graph_break_layernorm_count = r->graph_break_layernorm_count;
+        out_stats->graph_break_unknown_count = r->graph_break_unknown_count;
+        out_stats->first_graph_break_op_id = r->first_graph_break_op_id;
+        copy_str(out_stats->first_graph_break_op_name, sizeof(out_stats->first_graph_break_op_name),
+                 r->first_graph_break_op_name);
+        out_stats->compilability_score = r->compilability_score;
+        out_stats->autotune_loaded = model->autotune_loaded;
+        out_stats->autotune_saved = model->autotune_saved;
+        copy_str(out_stats->graph_break_summary, sizeof(out_stats->graph_break_summary), r->graph_break_summary);
+        out_stats->speculative_plan_count = a->spec_count;
+        out_stats->speculative_plan_hit = spec_hit;
+        out_stats->speculative_plan_miss_count = model->spec_misses;
+        out_stats->speculative_guard_miss_count = model->spec_guard_misses;
+        out_stats->speculative_confidence = a->spec_confidence;
+        copy_str(out_stats->speculative_shape_bucket, sizeof(out_stats->speculative_shape_bucket),
+                 bucket[0] ? bucket : a->spec_bucket);
+        out_stats->phantom_graph_enabled = ph->enabled;
+        out_stats->phantom_graph_match = phantom_hit;
+        out_stats->phantom_graph_match_count = ph->matches;
+        out_stats->phantom_graph_mismatch_count = ph->mismatches;
+        out_stats->phantom_graph_reshape_count = ph->reshapes;
+        out_stats->phantom_graph_confidence = ph->confidence;
+        out_stats->phantom_graph_match_score = phantom_sc;
+        copy_str(out_stats->phantom_graph_expected_bucket, sizeof(out_stats->phantom_graph_expected_bucket), ph->exp_bucket);
+        copy_str(out_stats->phantom_graph_expected_signature, sizeof(out_stats->phantom_graph_expected_signature),
+                 ph->exp_sig);
+        copy_str(out_stats->phantom_graph_observed_signature, sizeof(out_stats->phantom_graph_observed_signature),
+                 ph->obs_sig);
+    }
+    return error ? PYC_STATUS_RUNTIME_FAILED : PYC_STATUS_OK;
+}
+
+const char* pyc_model_last_decision_log(const pyc_compiled_model* model) {
+    return model ? model->log : "";
+}
+
+const pyc_collective_comm* pyc_model_distributed_comm(const pyc_compiled_model* model) {
+    (void)model;
+    return NULL;
+}
+
+pyc_comm_handle_t pyc_model_distributed_comm_handle(const pyc_compiled_model* model) {
+    (void)model;
+    return NULL;
+}
+
+void pyc_destroy_model(pyc_compiled_model* model) {
+    if (!model) {
+        return;
+    }
+    release_workspace(model);
+    free(model);
+}
