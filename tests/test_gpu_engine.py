@@ -1,0 +1,191 @@
+"""GPU: the full drop-in path pyc_compile_model -> pyc_run_model -> pyc_cuda_dispatch
+-> HIP kernels, with host buffers in and out, against the CPU oracle / the
+reference engine. PYC_HIP_STRICT=1 makes any CPU fallback a failure, and every
+test checks the execution path names the native HIP route."""
+import numpy as np
+import pytest
+
+import oracle
+from pyc_amd import abi
+from tests import engine_util as eu
+from tests.gpu_util import rel_max_err
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True)
+def _strict(monkeypatch, gpu):
+    for k in ("PYC_CUDA_SIMULATE_AVAILABLE", "PYC_CUDA_DISABLE", "PYC_CUDA_FORCE_FALLBACK", "PYC_CUDA_FORCE_ERROR",
+              "PYC_CUDA_SKIP_HOST_OUTPUT_COPY", "PYC_CUDA_ASSUME_STATIC_LHS", "PYC_CUDA_ASSUME_STATIC_RHS"):
+        monkeypatch.delenv(k, raising=False)
+    monkeypatch.setenv("PYC_HIP_STRICT", "1")
+
+
+def _native(stats):
+    path = stats.execution_path.decode()
+    assert path.startswith("hip_native"), path
+    assert stats.fallback_count == 0
+    return path
+
+
+def test_config1_through_run_model(monkeypatch):
+    """Config 1: one module in,in,in,matmul,add,relu,out (F32), X,W,bias ~ U(-1,1) seed 0.
+    Oracle: the reference engine's CPU executor + the reference CUDA path's
+    row-bias/ReLU epilogue; tolerance max|d|/max|ref| <= 1e-4."""
+    monkeypatch.setenv("PYC_CUDA_ASSUME_STATIC_RHS", "1")
+    r = np.random.default_rng(0)
+    x = r.uniform(-1, 1, (1024, 1024)).astype(np.float32)
+    w = r.uniform(-1, 1, (1024, 1024)).astype(np.float32)
+    b = r.uniform(-1, 1, 1024).astype(np.float32)
+    ops = [eu.op(abi.OP_INPUT, "x", (1024, 1024)), eu.op(abi.OP_INPUT, "w", (1024, 1024)),
+           eu.op(abi.OP_INPUT, "bias", (1024,)), eu.op(abi.OP_MATMUL, "matmul0", (), (0, 1)),
+           eu.op(abi.OP_ADD, "add0", (), (3, 2)), eu.op(abi.OP_RELU, "relu0", (), (4,)),
+           eu.op(abi.OP_OUTPUT, "out0", (1024, 1024), (5,))]
+    mdl = eu.Model(eu.mine(), ops, backend=abi.BACKEND_CUDA)
+    assert mdl.status == 0
+    ref = oracle.gemm_bias_relu_f32(x, w, b, relu=True, threads=8)
+    paths = []
+    for _ in range(3):
+        st, (out,), s = mdl.run([x, w, b], [(1024, 1024)])
+        assert st == 0
+        paths.append(_native(s))
+        assert rel_max_err(out, ref) <= 1e-4
+        assert s.cuda_kernel_ms > 0.0
+    mdl.close()
+    assert "graph_capture" in paths[0] and "graph_replay" in paths[-1], paths
+    assert "hip_gemm_f32" in paths[0]
+
+
+def test_bf16_matmul_module_nn():
+    m, k, n = 320, 256, 192
+    r = np.random.default_rng(1)
+    a = oracle.f32_to_bf16((r.standard_normal((m, k)) / 16).astype(np.float32))
+    b = oracle.f32_to_bf16(r.standard_normal((k, n)).astype(np.float32))
+    ops = [eu.op(abi.OP_INPUT, "a", (m, k), dtype=abi.DTYPE_BF16),
+           eu.op(abi.OP_INPUT, "b", (k, n), dtype=abi.DTYPE_BF16),
+           eu.op(abi.OP_MATMUL, "mm", (), (0, 1), dtype=abi.DTYPE_BF16),
+           eu.op(abi.OP_OUTPUT, "o", (m, n), (2,), dtype=abi.DTYPE_BF16)]
+    mdl = eu.Model(eu.mine(), ops, backend=abi.BACKEND_CUDA)
+    st, (out,), s = mdl.run([a, b], [(m, n)], in_dtypes=[abi.DTYPE_BF16] * 2, out_dtypes=[abi.DTYPE_BF16],
+                            out_np_dtype=np.uint16)
+    mdl.close()
+    assert st == 0
+    _native(s)
+    assert rel_max_err(oracle.bf16_to_f32(out), oracle.gemm_bf16(a, b, False)) <= 2e-2
+
+
+def test_matmul_chain_stays_on_gpu():
+    """A two-matmul MLP (matmul->add->relu->matmul) is one native plan; the
+    reference GPU path rejects more than one matmul (cuda_backend.c:1267-1272)."""
+    r = np.random.default_rng(2)
+    x = r.uniform(-1, 1, (64, 96)).astype(np.float32)
+    w1 = r.uniform(-1, 1, (96, 128)).astype(np.float32)
+    b1 = r.uniform(-1, 1, 128).astype(np.float32)
+    w2 = r.uniform(-1, 1, (128, 32)).astype(np.float32)
+    ops = [eu.op(abi.OP_INPUT, "x", (64, 96)), eu.op(abi.OP_INPUT, "w1", (96, 128)), eu.op(abi.OP_INPUT, "b1", (128,)),
+           eu.op(abi.OP_INPUT, "w2", (128, 32)), eu.op(abi.OP_MATMUL, "mm1", (), (0, 1)),
+           eu.op(abi.OP_ADD, "add1", (), (4, 2)), eu.op(abi.OP_RELU, "relu1", (), (5,)),
+           eu.op(abi.OP_MATMUL, "mm2", (), (6, 3)), eu.op(abi.OP_OUTPUT, "o", (64, 32), (7,))]
+    mdl = eu.Model(eu.mine(), ops, backend=abi.BACKEND_CUDA)
+    st, (out,), s = mdl.run([x, w1, b1, w2], [(64, 32)])
+    mdl.close()
+    assert st == 0
+    _native(s)
+    h = oracle.gemm_bias_relu_f32(x, w1, b1, relu=True)
+    assert rel_max_err(out, oracle.matmul_f32(h, w2)) <= 1e-4
+
+
+def test_decode_chain_module_fp8():
+    """Two decode layers (up: fp8 [F,D] + scale, ReLU; down: fp8 [D,F] + scale) in one module."""
+    M, D, F = 32, 256, 512
+    r = np.random.default_rng(3)
+    x = oracle.f32_to_bf16(r.standard_normal((M, D)).astype(np.float32))
+    layers, ops, ins = [], [eu.op(abi.OP_INPUT, "x", (M, D), dtype=abi.DTYPE_BF16)], [x]
+    dts = [abi.DTYPE_BF16]
+    cur = 0
+    for l in range(2):
+        wu, su = oracle.quantize_e4m3_per_col((r.standard_normal((D, F)) * np.sqrt(2 / D)).astype(np.float32))
+        wd, sd = oracle.quantize_e4m3_per_col((r.standard_normal((F, D)) * np.sqrt(2 / F)).astype(np.float32))
+        layers.append((wu, su, wd, sd))
+        base = len(ops)
+        ops += [eu.op(abi.OP_INPUT, f"wu{l}", (F, D), dtype=abi.DTYPE_FP8_E4M3),
+                eu.op(abi.OP_INPUT, f"su{l}", (F,)),
+                eu.op(abi.OP_INPUT, f"wd{l}", (D, F), dtype=abi.DTYPE_FP8_E4M3),
+                eu.op(abi.OP_INPUT, f"sd{l}", (D,))]
+        ins += [wu, su, wd, sd]
+        dts += [abi.DTYPE_FP8_E4M3, abi.DTYPE_F32, abi.DTYPE_FP8_E4M3, abi.DTYPE_F32]
+        ops += [eu.op(abi.OP_MATMUL, f"up{l}", (), (cur, base, base + 1), dtype=abi.DTYPE_BF16),
+                eu.op(abi.OP_RELU, f"relu{l}", (), (base + 4,), dtype=abi.DTYPE_BF16),
+                eu.op(abi.OP_MATMUL, f"down{l}", (), (base + 5, base + 2, base + 3), dtype=abi.DTYPE_BF16)]
+        cur = base + 6
+    ops.append(eu.op(abi.OP_OUTPUT, "y", (M, D), (cur,), dtype=abi.DTYPE_BF16))
+    mdl = eu.Model(eu.mine(), ops, backend=abi.BACKEND_CUDA)
+    assert mdl.status == 0
+    st, (out,), s = mdl.run(ins, [(M, D)], in_dtypes=dts, out_dtypes=[abi.DTYPE_BF16], out_np_dtype=np.uint16)
+    mdl.close()
+    assert st == 0
+    assert "hip_gemm_w8a16_e4m3" in _native(s)
+    ref = oracle.bf16_to_f32(oracle.w8a16_chain(x, layers))
+    assert rel_max_err(oracle.bf16_to_f32(out), ref) <= 2e-2
+
+
+def test_conv_and_attention_modules():
+    r = np.random.default_rng(4)
+    x = oracle.f32_to_bf16(r.uniform(0, 1, (2, 8, 8, 16)).astype(np.float32))
+    w = oracle.f32_to_bf16(r.normal(0, 0.1, (32, 3, 3, 16)).astype(np.float32))
+    bias = r.normal(0, 0.1, 32).astype(np.float32)
+    ops = [eu.op(abi.OP_INPUT, "x", (2, 8, 8, 16), dtype=abi.DTYPE_BF16),
+           eu.op(abi.OP_INPUT, "w", (32, 3, 3, 16), dtype=abi.DTYPE_BF16),
+           eu.op(abi.OP_INPUT, "bias", (32,)),
+           eu.op(abi.OP_CONV2D, "conv@s1x1p1x1", (), (0, 1), dtype=abi.DTYPE_BF16),
+           eu.op(abi.OP_ADD, "add", (), (3, 2), dtype=abi.DTYPE_BF16),
+           eu.op(abi.OP_RELU, "relu", (), (4,), dtype=abi.DTYPE_BF16),
+           eu.op(abi.OP_OUTPUT, "y", (2, 8, 8, 32), (5,), dtype=abi.DTYPE_BF16)]
+    mdl = eu.Model(eu.mine(), ops, backend=abi.BACKEND_CUDA)
+    st, (out,), s = mdl.run([x, w, bias], [(2, 8, 8, 32)], in_dtypes=[abi.DTYPE_BF16, abi.DTYPE_BF16, abi.DTYPE_F32],
+                            out_dtypes=[abi.DTYPE_BF16], out_np_dtype=np.uint16)
+    mdl.close()
+    assert st == 0 and "hip_conv2d_bf16" in _native(s)
+    ref = oracle.conv2d_nhwc_f32(oracle.bf16_to_f32(x), oracle.bf16_to_f32(w), bias, (1, 1), (1, 1), True)
+    assert rel_max_err(oracle.bf16_to_f32(out), ref) <= 2e-2
+
+    q, k, v = (oracle.f32_to_bf16(r.standard_normal((1, 2, 96, 64)).astype(np.float32)) for _ in range(3))
+    ops = [eu.op(abi.OP_INPUT, n, (1, 2, 96, 64), dtype=abi.DTYPE_BF16) for n in ("q", "k", "v")]
+    ops += [eu.op(abi.OP_ATTENTION, "attn_causal", (), (0, 1, 2), dtype=abi.DTYPE_BF16),
+            eu.op(abi.OP_OUTPUT, "o", (1, 2, 96, 64), (3,), dtype=abi.DTYPE_BF16)]
+    mdl = eu.Model(eu.mine(), ops, backend=abi.BACKEND_CUDA)
+    st, (out,), s = mdl.run([q, k, v], [(1, 2, 96, 64)], in_dtypes=[abi.DTYPE_BF16] * 3,
+                            out_dtypes=[abi.DTYPE_BF16], out_np_dtype=np.uint16)
+    mdl.close()
+    assert st == 0 and "hip_attention_bf16" in _native(s)
+    ref = oracle.attention_f32(*(oracle.bf16_to_f32(t) for t in (q, k, v)), True, 1 / 8)
+    assert rel_max_err(oracle.bf16_to_f32(out), ref) <= 2e-2
+
+
+def test_no_graph_and_skip_output_copy(monkeypatch):
+    monkeypatch.setenv("PYC_CUDA_ENABLE_GRAPH_REPLAY", "0")
+    r = np.random.default_rng(5)
+    a = r.uniform(-1, 1, (40, 24)).astype(np.float32)
+    b = r.uniform(-1, 1, (24, 16)).astype(np.float32)
+    ops = [eu.op(abi.OP_INPUT, "a", (40, 24)), eu.op(abi.OP_INPUT, "b", (24, 16)),
+           eu.op(abi.OP_MATMUL, "mm", (), (0, 1)), eu.op(abi.OP_OUTPUT, "o", (40, 16), (2,))]
+    mdl = eu.Model(eu.mine(), ops, backend=abi.BACKEND_CUDA)
+    st, (out,), s = mdl.run([a, b], [(40, 16)])
+    assert st == 0 and _native(s).startswith("hip_native:")
+    assert rel_max_err(out, oracle.matmul_f32(a, b)) <= 1e-4
+    monkeypatch.setenv("PYC_CUDA_SKIP_HOST_OUTPUT_COPY", "1")
+    st, (out2,), s = mdl.run([a, b], [(40, 16)])
+    mdl.close()
+    assert st == 0 and not out2.any()  # output left untouched, as the reference does
+
+
+def test_bf16_passthrough_native():
+    data = np.array([0x3F80, 0x4000, 0x4040, 0x4080], np.uint16)
+    ops = [eu.op(abi.OP_INPUT, "in", (4,), dtype=abi.DTYPE_BF16), eu.op(abi.OP_OUTPUT, "o", (4,), (0,),
+                                                                         dtype=abi.DTYPE_BF16)]
+    mdl = eu.Model(eu.mine(), ops, backend=abi.BACKEND_CUDA)
+    st, (out,), s = mdl.run([data], [(4,)], in_dtypes=[abi.DTYPE_BF16], out_dtypes=[abi.DTYPE_BF16],
+                            out_np_dtype=np.uint16)
+    mdl.close()
+    assert st == 0 and out.tolist() == data.tolist()
+    _native(s)
