@@ -24,6 +24,8 @@
 int pyc_hip_gemm_half_launch(int is_bf16, int b_trans, int tile, int M, int N, int K,
                              const void* A, const void* B, void* C, float alpha, float beta,
                              const float* bias, int epi, void* stream);
+int pyc_hip_gemm_nt_lds_launch(int is_bf16, int M, int N, int K, const void* A, const void* B, void* C,
+                               float alpha, float beta, const float* bias, int epi, void* stream);
 int pyc_hip_gemm_f32_launch(int b_trans, int M, int N, int K, const void* A, const void* B,
                             void* C, float alpha, float beta, const float* bias, int epi,
                             void* stream);
@@ -46,7 +48,7 @@ typedef struct {
     int kind;
     int dtype;
     int b_trans;  /* GEMM: B stored [N,K] */
-    int tile;     /* GEMM half tile edge; 0 = choose by shape */
+    int tile;     /* GEMM half tile edge; 0 = choose by shape; -1 = direct-LDS 8-wave NT kernel */
     int unit_epilogue_only; /* alpha must be 1 and beta 0 */
     int priority;
     double occupancy;      /* waves per SIMD / 8 for the variant's launch bounds */
@@ -57,6 +59,7 @@ typedef struct {
 
 static const hip_variant k_variants[] = {
     /* bf16 MFMA GEMM tiles */
+    {"matmul", "hip_gemm_bf16_nt_256x256_lds8", VK_GEMM, VT_BF16, 1, -1, 0, 125, 0.25, 131072, 2, PYC_KERNEL_WORKLOAD_LARGE_SQUARE},
     {"matmul", "hip_gemm_bf16_nt_256x256", VK_GEMM, VT_BF16, 1, 256, 0, 120, 0.125, 131072, 3, PYC_KERNEL_WORKLOAD_LARGE_SQUARE},
     {"matmul", "hip_gemm_bf16_nt_128x128", VK_GEMM, VT_BF16, 1, 128, 0, 110, 0.25, 65536, 2, PYC_KERNEL_WORKLOAD_SQUARE},
     {"matmul", "hip_gemm_bf16_nn_256x256", VK_GEMM, VT_BF16, 0, 256, 0, 115, 0.125, 131072, 3, PYC_KERNEL_WORKLOAD_LARGE_SQUARE},
@@ -137,7 +140,16 @@ static int gemm_run(const hip_variant* v, int M, int N, int K, const void* A, co
     if (v->dtype == VT_F32) {
         return pyc_hip_gemm_f32_launch(v->b_trans, M, N, K, A, B, C, alpha, beta, bias, epilogue, stream);
     }
-    return pyc_hip_gemm_half_launch(v->dtype == VT_BF16, v->b_trans, v->tile ? v->tile : pick_half_tile(M, N),
+    /* The direct-LDS NT kernel takes large NT shapes with K % 64 == 0 (its
+     * launcher answers 1 when the shape is outside its preconditions). */
+    if (v->b_trans && (v->tile == -1 || (v->tile == 0 && pick_half_tile(M, N) == 256))) {
+        const int rc = pyc_hip_gemm_nt_lds_launch(v->dtype == VT_BF16, M, N, K, A, B, C, alpha, beta, bias,
+                                                  epilogue, stream);
+        if (rc != 1) {
+            return rc;
+        }
+    }
+    return pyc_hip_gemm_half_launch(v->dtype == VT_BF16, v->b_trans, v->tile > 0 ? v->tile : pick_half_tile(M, N),
                                     M, N, K, A, B, C, alpha, beta, bias, epilogue, stream);
 }
 

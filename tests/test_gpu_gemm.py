@@ -37,14 +37,16 @@ def _check_half(got_bits, ref, k):
 
 
 SHAPES = [(256, 256, 64), (512, 768, 256), (300, 200, 72), (1, 1, 8), (33, 65, 40),
-          (1024, 1024, 1024), (130, 257, 520)]
+          (1024, 1024, 1024), (130, 257, 520), (700, 300, 192), (4096, 4096, 512)]
 
 
 @pytest.mark.parametrize("m,n,k", SHAPES)
 @pytest.mark.parametrize("layout", ["nt", "nn"])
-@pytest.mark.parametrize("tile", ["", "_128x128", "_256x256"])
+@pytest.mark.parametrize("tile", ["", "_128x128", "_256x256", "_256x256_lds8"])
 def test_bf16_gemm_vs_oracle(gpu, m, n, k, layout, tile):
     torch = gpu
+    if tile.endswith("lds8") and layout == "nn":
+        pytest.skip("the direct-LDS kernel is NT only")
     bt = layout == "nt"
     a, b = _bf16_inputs(m, n, k, m * 7 + n + k, bt)
     A, B = dev_bits16(torch, a), dev_bits16(torch, b)
