@@ -59,7 +59,7 @@ typedef struct {
 
 static const hip_variant k_variants[] = {
     /* bf16 MFMA GEMM tiles */
-    {"matmul", "hip_gemm_bf16_nt_256x256_lds8", VK_GEMM, VT_BF16, 1, -1, 0, 125, 0.25, 131072, 2, PYC_KERNEL_WORKLOAD_LARGE_SQUARE},
+    {"matmul", "hip_gemm_bf16_nt_256x256_lds", VK_GEMM, VT_BF16, 1, -1, 0, 125, 0.25, 131072, 2, PYC_KERNEL_WORKLOAD_LARGE_SQUARE},
     {"matmul", "hip_gemm_bf16_nt_256x256", VK_GEMM, VT_BF16, 1, 256, 0, 120, 0.125, 131072, 3, PYC_KERNEL_WORKLOAD_LARGE_SQUARE},
     {"matmul", "hip_gemm_bf16_nt_128x128", VK_GEMM, VT_BF16, 1, 128, 0, 110, 0.25, 65536, 2, PYC_KERNEL_WORKLOAD_SQUARE},
     {"matmul", "hip_gemm_bf16_nn_256x256", VK_GEMM, VT_BF16, 0, 256, 0, 115, 0.125, 131072, 3, PYC_KERNEL_WORKLOAD_LARGE_SQUARE},
@@ -67,6 +67,7 @@ static const hip_variant k_variants[] = {
     {"matmul", "hip_gemm_bf16_nt", VK_GEMM, VT_BF16, 1, 0, 0, 100, 0.125, 131072, 3, PYC_KERNEL_WORKLOAD_ANY},
     {"matmul", "hip_gemm_bf16_nn", VK_GEMM, VT_BF16, 0, 0, 0, 100, 0.125, 131072, 3, PYC_KERNEL_WORKLOAD_ANY},
     /* fp16 MFMA GEMM */
+    {"matmul", "hip_gemm_f16_nt_256x256_lds", VK_GEMM, VT_F16, 1, -1, 0, 96, 0.25, 131072, 2, PYC_KERNEL_WORKLOAD_LARGE_SQUARE},
     {"matmul", "hip_gemm_f16_nt", VK_GEMM, VT_F16, 1, 0, 0, 95, 0.125, 131072, 3, PYC_KERNEL_WORKLOAD_ANY},
     {"matmul", "hip_gemm_f16_nn", VK_GEMM, VT_F16, 0, 0, 0, 95, 0.125, 131072, 3, PYC_KERNEL_WORKLOAD_ANY},
     /* fp32 MFMA GEMM (true fp32) */

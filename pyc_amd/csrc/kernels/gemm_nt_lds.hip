@@ -1,82 +1,166 @@
-// gemm_nt_lds.hip — bf16/fp16 "NT" GEMM (A [M,K], B [N,K], both K-contiguous)
-// with direct global->LDS loads, the large-shape kernel of the benchmark
-// (8192^3, reference cfg: gemm/kernel.cu:71-84 semantics with column-major B).
+// gemm_nt_lds.hip — bf16/fp16 "NT" GEMM (A [M,K] and B [N,K], both K-contiguous,
+// C [M,N] row-major): the large-shape kernels behind the reference's
+// gemm/kernel.cu:71-84 entry point (C = alpha*A*B^T + beta*C, plus the
+// bias/ReLU epilogue of compiler_api.c's fused MATMUL->ADD->RELU).
 //
-// Differences from the register-staged mainloop in gemm_core.hpp:
-//  * global_load_lds_dwordx4: each lane's 16 bytes land in LDS at
-//    (wave base + 16*lane) without passing through VGPRs, so no staging
-//    registers and no ds_write instructions. The XOR-swizzled LDS layout is
-//    obtained by choosing, per lane, which 16-byte global chunk it fetches:
-//    LDS slot (row, p) receives global chunk (row, p ^ (row & 7)).
-//  * 8 waves (2 per SIMD) in a 2 x 4 grid, each owning a 128 x 64 sub-tile, so
-//    one wave's LDS-read latency hides behind the other wave's MFMAs.
-//  * One barrier per K step: wait for this wave's loads of step k, barrier
-//    (all loads of k visible, everyone done with step k-1), then issue the
-//    loads of step k+1 into the buffer step k-1 used, then the MFMAs of step k.
-// Preconditions (checked by the launcher): K % 64 == 0. Rows of A/B past M/N
-// are clamped to the last valid row; their products only reach output rows
-// and columns that the epilogue does not store.
+// Shape of the computation on a CU (gfx950: 4 SIMDs, 160 KB LDS):
+//  * 256 x 256 C tile per workgroup, 4 waves (one per SIMD), each wave a
+//    128 x 128 sub-tile = 8 x 8 fragments of v_mfma_f32_16x16x32_{bf16,f16}.
+//    A wave tile of TM x TN reads (TM + TN) * BK * 2 bytes of LDS per K step
+//    for TM * TN / 256 MFMAs; 128 x 128 keeps LDS reads at 128 KB per
+//    256 x 256 x 64 step, below the LDS port's rate at full MFMA issue.
+//  * K stages of 64: every A/B row segment a stage needs is one whole
+//    128-byte line, moved global -> LDS by buffer_load_dwordx4 ... lds
+//    (no VGPR staging, no ds_write). Two stages (128 KB) double-buffer.
+//  * The XOR-swizzled LDS layout (16-byte chunk c of row r stored at
+//    c ^ (r & 7)) is produced by choosing which global chunk each lane
+//    fetches, and makes the fragment reads bank-conflict free.
+//  * The MFMA stream of each K step is laid out by hand (sched_barrier) with
+//    the fragment reads and DMA issues threaded between MFMAs; two barriers
+//    per step separate "buffer free" from "next stage visible".
+//  * The MFMA computes B * A^T so each lane ends with four adjacent columns
+//    of C; the epilogue stages rounded values through LDS and writes whole
+//    256-byte row segments with 16-byte stores.
+// Rows of A/B past M/N are clamped to the last valid row; their products only
+// reach rows and columns of C that are never stored.
+#include <stdint.h>
 #include <stdlib.h>
+
+#include <type_traits>
 
 #include "common.hpp"
 
 namespace pyc {
 
-// One 16-byte-per-lane LDS-DMA load: lane i's 16 bytes from `src` land at LDS
-// byte address lds_base + 16*i. Written as inline asm so the compiler does not
-// treat every later LDS read as dependent on it (it would insert a full
-// vmcnt(0) wait right after the issue and serialise loads with the MFMAs); the
-// kernel waits for these loads itself, before the barrier that publishes them.
-// M0 carries the wave-uniform LDS base; nothing else in these kernels uses M0.
-__device__ inline void lds_dma_b128(const void* src, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+// One LDS-DMA load: lane i's 16 bytes at buffer offset voff + soff land at
+// LDS byte address lds_base + 16*i. Written as inline asm so the compiler does
+// not treat every later LDS read as dependent on it (it would insert a full
+// vmcnt(0) wait after each issue and serialise the loads with the MFMAs); the
+// kernels wait for these loads themselves, before the barrier that publishes
+// them. M0 carries the wave-uniform LDS base; nothing else here uses M0.
+// Offsets at or past the descriptor's byte count read zero.
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+__device__ inline void lds_dma_buf_b128(i32x4 rsrc, uint32_t voff, uint32_t soff, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                  :
-                 : "s"(lds_base), "v"(src)
+                 : "s"(lds_base), "v"(voff), "s"(rsrc), "s"(soff)
                  : "memory", "m0");
 }
 
-__device__ inline void wait_vmem_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-
-constexpr int kD_BM = 256, kD_BN = 256;
-
-// LDS slot of logical 16-byte chunk `chunk` in row `row`. 128-byte rows (8
-// chunks): XOR with row & 7. 64-byte rows (4 chunks): four rows share a
-// 256-byte bank window, so XOR with (row >> 2) & 3. Either way the 16 rows read
-// by one 16-lane group at equal k hit 16 different 16-byte bank groups.
-__device__ inline int d_swz(int row, int chunk, int nchunks) {
-    return nchunks == 8 ? (chunk ^ (row & 7)) : (chunk ^ ((row >> 2) & 3));
+// Raw buffer descriptor (CDNA layout): 48-bit base, stride 0, byte count,
+// 32-bit data format. Every field is wave-uniform.
+__device__ inline i32x4 make_buf_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)(uintptr_t)base;
+    i32x4 r;
+    r.x = __builtin_amdgcn_readfirstlane((int32_t)(uint32_t)a);
+    r.y = __builtin_amdgcn_readfirstlane((int32_t)((uint32_t)(a >> 32) & 0xFFFFu));
+    r.z = __builtin_amdgcn_readfirstlane((int32_t)bytes);
+    r.w = 0x00020000;
+    return r;
 }
 
 template <int N> __device__ inline void wait_vmem_le() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// BK: K extent of one LDS stage (32 or 64); STAGES: LDS buffers (STAGES-1
-// stages of global loads in flight while one is consumed).
-template <typename T, int BK, int STAGES, bool XPREFETCH, int kD_WAVES>
-__global__ void __launch_bounds__(kD_WAVES * kWave, 1)
-gemm_nt_lds_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
-                   uint16_t* __restrict__ C, int M, int N, int K, float alpha, float beta,
-                   const float* __restrict__ bias, int epi, int tiles_m, int tiles_n, int group_m) {
-    constexpr int kD_NT = kD_WAVES * kWave;
-    constexpr int WN = kD_WAVES / 2;              // waves along N (2 along M)
-    constexpr int TN = kD_BN / WN;                // wave tile columns (64 or 128)
-    constexpr int FN = TN / 16;                   // 16-wide B fragments per wave
-    constexpr int CH = BK / 8;                    // 16-byte chunks per LDS row
-    constexpr int ROWS_PER_LOAD = kWave / CH;     // LDS rows one wave-load fills
-    constexpr int LOADS = kD_BM * CH / kD_NT;     // loads per thread per operand per stage
-    constexpr int LPT = 2 * LOADS;                // vmem instructions per thread per stage
-    static_assert(LOADS * kD_NT == kD_BM * CH, "load split");
-    __shared__ __attribute__((aligned(1024))) uint16_t As[STAGES][kD_BM * BK];
-    __shared__ __attribute__((aligned(1024))) uint16_t Bs[STAGES][kD_BN * BK];
+constexpr int kD_BM = 256, kD_BN = 256;
+
+// LDS slot of logical 16-byte chunk `chunk` in a 128-byte stage row `row`.
+// A fragment read has 16 lanes on 16 consecutive rows at one logical chunk;
+// the XOR spreads them over all 16 bank groups of a 256-byte bank window
+// (rocprofv3 SQ_LDS_BANK_CONFLICT reads 0 for these kernels).
+__device__ inline int d_swz(int row, int chunk) { return chunk ^ (row & 7); }
+
+// Epilogue of one wave's 128 x 128 tile whose accumulators hold transposed
+// 16 x 16 blocks (the MFMA computed B*A^T): lane l's acc[i][j][e] is tile
+// element (16i + l%16, 16j + 4*(l/16) + e), i.e. four adjacent columns.
+// Phase 1 applies alpha/beta/bias/ReLU, rounds, and writes 8 bytes per
+// fragment into a wave-private 32 KB LDS area laid out row-major (256-byte
+// rows, 16-byte chunk c of row r at chunk c ^ (r & 15), so the 16 rows one
+// write instruction touches fall into different banks). Phase 2 reads whole
+// 16-byte chunks back and writes each 256-byte row segment with 16 lanes of
+// 16-byte stores instead of 2-byte scattered ones.
+template <typename T>
+__device__ inline void store_tile_128x128_t(const f32x4 (&acc)[8][8], uint16_t* stage, uint16_t* __restrict__ C,
+                                            int M, int N, int row0, int col0, float alpha, float beta,
+                                            const float* __restrict__ bias, int epi, int lane) {
+    const int lr = lane & 15;
+    const int lg = lane >> 4;
+    const bool has_bias = (epi & 1) && bias != nullptr;
+    const bool relu = (epi & 2) != 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int c = 16 * j + 4 * lg;  // first of this lane's 4 tile columns
+        float bv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bv[e] = (has_bias && col0 + c + e < N) ? bias[col0 + c + e] : 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int r = 16 * i + lr;
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[e] = alpha * acc[i][j][e];
+                if (beta != 0.f) {
+                    const int gm = row0 + r, gn = col0 + c + e;
+                    if (gm < M && gn < N) v[e] += beta * elem<T>::to_f32(C[(size_t)gm * N + gn]);
+                }
+                v[e] += bv[e];
+                if (relu) v[e] = v[e] > 0.f ? v[e] : 0.f;
+            }
+            uint2 packed;
+            packed.x = (uint32_t)elem<T>::from_f32(v[0]) | ((uint32_t)elem<T>::from_f32(v[1]) << 16);
+            packed.y = (uint32_t)elem<T>::from_f32(v[2]) | ((uint32_t)elem<T>::from_f32(v[3]) << 16);
+            const int phys = r * 128 + (((c >> 3) ^ (r & 15)) << 3) + (c & 4);
+            *reinterpret_cast<uint2*>(stage + phys) = packed;
+        }
+    }
+    const bool vec = (N % 8 == 0) && (((uintptr_t)C & 15) == 0);
+#pragma unroll 4
+    for (int p = 0; p < 32; ++p) {
+        const int r = 4 * p + lg;
+        const uint4 val = *reinterpret_cast<const uint4*>(stage + r * 128 + ((lr ^ (r & 15)) << 3));
+        const int gm = row0 + r;
+        const int gn = col0 + lr * 8;
+        if (gm >= M) continue;
+        uint16_t* dst = C + (size_t)gm * N + gn;
+        if (vec && gn + 8 <= N) {
+            *reinterpret_cast<uint4*>(dst) = val;
+        } else {
+            const uint32_t w[4] = {val.x, val.y, val.z, val.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (gn + e < N) dst[e] = (uint16_t)(w[e >> 1] >> ((e & 1) * 16));
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// One-shot kernel (one workgroup per tile): any M, N; K % 64 == 0.
+// Two 64 KB stages fill 128 KB of LDS, so a stage's loads are in flight for
+// about one step; two barriers per step separate "buffer free" from "next
+// stage visible" (see the step schedule below).
+// Preconditions: K % 64 == 0, M*K*2 and N*K*2 below 2^32 (buffer byte counts).
+template <typename T, int GA, int GB>
+__global__ void __launch_bounds__(256, 1)
+gemm_nt_lds4k64_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
+                       uint16_t* __restrict__ C, int M, int N, int K, float alpha, float beta,
+                       const float* __restrict__ bias, int epi, int tiles_m, int tiles_n, int group_m) {
+    constexpr int BK = 64, CH = 8, NT = 256;
+    constexpr int ROWS_PER_LOAD = kWave / CH;       // 8 LDS rows per wave-load
+    constexpr int LOADS = kD_BM * CH / NT;          // 8 per operand per stage
+    constexpr uint32_t STAGE_BYTES = kD_BM * BK * 2;  // 32 KB per operand
+    // stages 0/1 of A, then of B; reused after the K loop to stage C
+    __shared__ __attribute__((aligned(1024))) uint16_t smem[2 * (kD_BM + kD_BN) * BK];
+    uint16_t* const As = smem;
+    uint16_t* const Bs = smem + 2 * kD_BM * BK;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int wm = wave / WN;  // 0..1 -> 128-row half
-    const int wn = wave % WN;  // TN-column slice
+    const int wm = wave >> 1;
+    const int wn = wave & 1;
 
-    // tile order: XCD-contiguous ranges, grouped by GROUP_M tile rows
     int bid = blockIdx.x;
     const int nblk = gridDim.x;
     if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
@@ -88,175 +172,401 @@ gemm_nt_lds_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ 
     const int m0 = (first_m + in % gsz) * kD_BM;
     const int n0 = (in / gsz) * kD_BN;
 
-    // Load j of wave w fills LDS rows r0 = (j*8 + w)*ROWS_PER_LOAD ..; lane l ->
-    // row r0 + l/CH, physical chunk l%CH holding logical chunk (l%CH) ^ row.
-    const int lrowc = lane / CH;
-    const int pch = lane % CH;
-    const uint16_t* a_src[LOADS];
-    const uint16_t* b_src[LOADS];
+    // DMA load j (< LOADS: A, else B) fills LDS rows (j%LOADS * 4 + wave) * 8
+    // + lane/8, physical chunk lane%8 holding logical chunk (lane%8) ^ (row&7).
+    const uint32_t as_base = (uint32_t)(uintptr_t)&As[0];
+    const uint32_t bs_base = (uint32_t)(uintptr_t)&Bs[0];
+    const i32x4 a_rsrc = make_buf_rsrc(A, (uint32_t)((size_t)M * K * 2));
+    const i32x4 b_rsrc = make_buf_rsrc(B, (uint32_t)((size_t)N * K * 2));
+    uint32_t voff[2 * LOADS];
+    uint32_t ldso[2 * LOADS];
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
-        const int row = (j * kD_WAVES + wave) * ROWS_PER_LOAD + lrowc;
-        const int lch = d_swz(row, pch, CH);
-        a_src[j] = A + (size_t)min(m0 + row, M - 1) * K + lch * 8;
-        b_src[j] = B + (size_t)min(n0 + row, N - 1) * K + lch * 8;
+        const int row = (j * 4 + wave) * ROWS_PER_LOAD + lane / CH;
+        const int lch = d_swz(row, lane % CH);
+        voff[j] = (uint32_t)(((size_t)min(m0 + row, M - 1) * K + lch * 8) * 2);
+        voff[LOADS + j] = (uint32_t)(((size_t)min(n0 + row, N - 1) * K + lch * 8) * 2);
+        const uint32_t off = (uint32_t)((j * 4 + wave) * ROWS_PER_LOAD * BK * 2);
+        ldso[j] = __builtin_amdgcn_readfirstlane(as_base + off);
+        ldso[LOADS + j] = __builtin_amdgcn_readfirstlane(bs_base + off);
     }
-    const uint32_t as_base = (uint32_t)(uintptr_t)&As[0][0];
-    const uint32_t bs_base = (uint32_t)(uintptr_t)&Bs[0][0];
-    auto issue = [&](int kt, int buf) {
-        const int k0 = kt * BK;
-#pragma unroll
-        for (int j = 0; j < LOADS; ++j) {
-            const uint32_t off = (uint32_t)(((j * kD_WAVES + wave) * ROWS_PER_LOAD * BK + buf * kD_BM * BK) * 2);
-            lds_dma_b128(a_src[j] + k0, __builtin_amdgcn_readfirstlane(as_base + off));
-            lds_dma_b128(b_src[j] + k0, __builtin_amdgcn_readfirstlane(bs_base + off));
-        }
+    auto dma = [&](int j, int kt, int buf) {
+        lds_dma_buf_b128(j < LOADS ? a_rsrc : b_rsrc, voff[j], (uint32_t)(kt * BK * 2),
+                         ldso[j] + (uint32_t)buf * STAGE_BYTES);
     };
 
-    f32x4 acc[8][FN];
+    // Fragment i of k-half h: rows wm*128 + 16i + lane%16, logical chunk
+    // 4h + lane/16, physical chunk (4h + lane/16) ^ (lane & 7) -> i*2048 apart.
+    const int lrow = lane & 15;
+    const int lgrp = lane >> 4;
+    const uint16_t* a_rd[2];
+    const uint16_t* b_rd[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int pc = (h * 4 + lgrp) ^ (lrow & 7);
+        a_rd[h] = As + (wm * 128 + lrow) * BK + pc * 8;
+        b_rd[h] = Bs + (wn * 128 + lrow) * BK + pc * 8;
+    }
+
+    f32x4 acc[8][8];
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+    u32x4 fa[2][8], fb[2][8];
     const int ktiles = K / BK;
-    const int lrow = lane & 15;
-    const int lgrp = lane >> 4;
-    auto read_frags = [&](int buf, int kk, u32x4* af, u32x4* bfr) {
-        const uint16_t* as = As[buf];
-        const uint16_t* bs = Bs[buf];
-        const int ch = kk * 4 + lgrp;
+
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int r = wm * 128 + i * 16 + lrow;
-            af[i] = *reinterpret_cast<const u32x4*>(&as[r * BK + d_swz(r, ch, CH) * 8]);
-        }
+    for (int j = 0; j < 2 * LOADS; ++j) dma(j, 0, 0);
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            const int r = wn * TN + j * 16 + lrow;
-            bfr[j] = *reinterpret_cast<const u32x4*>(&bs[r * BK + d_swz(r, ch, CH) * 8]);
+    for (int j = 0; j < 2 * LOADS; ++j) dma(j, min(1, ktiles - 1), 1);
+    wait_vmem_le<2 * LOADS>();  // stage 0 landed; stage 1 may be in flight
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        fa[0][i] = *reinterpret_cast<const u32x4*>(a_rd[0] + i * 16 * BK);
+        fb[0][i] = *reinterpret_cast<const u32x4*>(b_rd[0] + i * 16 * BK);
+    }
+
+    // One K step = 64 groups of 2 MFMAs: groups 0..31 on fa/fb[0] = (kt, k
+    // 0..31), groups 32..63 on fa/fb[1] = (kt, k 32..63). Events:
+    //   groups 0..15      read (kt, k 32..63) into set 1 from buffer kt%2
+    //   group GA          own reads done, barrier A: buffer kt%2 is free
+    //   groups GA..GA+15  DMA of step kt+2 into buffer kt%2
+    //   group GB          own DMA of kt+1 landed, barrier B: kt+1 visible
+    //   groups GB..GB+15  read (kt+1, k 0..31) into set 0 from buffer (kt+1)%2
+    // so a stage's loads have from group GA of one step to group GB of the
+    // next to land.
+    static_assert(GA >= 16 && GA + 16 <= GB && GB >= 32 && GB + 16 <= 64, "event order");
+    auto step = [&](int kt) {
+        const uint32_t cur = (uint32_t)(kt & 1) * (kD_BM * BK);
+        const uint32_t nxt = (uint32_t)((kt + 1) & 1) * (kD_BM * BK);
+        const int dkt = min(kt + 2, ktiles - 1);
+        const int dbuf = kt & 1;
+#pragma unroll
+        for (int g = 0; g < 64; ++g) {
+            if (g == GA) {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                __syncthreads();
+            }
+            if (g == GB) {
+                wait_vmem_le<2 * LOADS>();
+                __syncthreads();
+            }
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const int m = (g & 31) * 2 + t;
+                const int i = m >> 3, j = m & 7;
+                // B fragment as the row operand: acc holds C^T blocks (see epilogue)
+                if (g < 32) acc[i][j] = mfma16x16x32(fb[0][j], fa[0][i], acc[i][j], T{});
+                else acc[i][j] = mfma16x16x32(fb[1][j], fa[1][i], acc[i][j], T{});
+            }
+            if (g < 16) {
+                const int f = g >> 1;
+                if ((g & 1) == 0) fa[1][f] = *reinterpret_cast<const u32x4*>(a_rd[1] + cur + f * 16 * BK);
+                else fb[1][f] = *reinterpret_cast<const u32x4*>(b_rd[1] + cur + f * 16 * BK);
+            }
+            if (g >= GA && g < GA + 16) dma(g - GA, dkt, dbuf);
+            if (g >= GB && g < GB + 16) {
+                const int f = (g - GB) >> 1;
+                if (((g - GB) & 1) == 0) fa[0][f] = *reinterpret_cast<const u32x4*>(a_rd[0] + nxt + f * 16 * BK);
+                else fb[0][f] = *reinterpret_cast<const u32x4*>(b_rd[0] + nxt + f * 16 * BK);
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
     };
-    auto mfma_block = [&](const u32x4* af, const u32x4* bfr) {
+    for (int kt = 0; kt < ktiles; ++kt) step(kt);
+    wait_vmem_le<0>();  // every DMA write (including the last, unused ones) has landed ...
+    __syncthreads();    // ... for all waves, and no wave reads A/B fragments any more
+    store_tile_128x128_t<T>(acc, smem + wave * (128 * 128), C, M, N, m0 + wm * 128, n0 + wn * 128, alpha,
+                            beta, bias, epi, lane);
+}
+
+// ---------------------------------------------------------------------------
+// Persistent form of the 4-wave BK = 64 kernel: one workgroup per CU walks
+// tiles blockIdx.x, blockIdx.x + gridDim.x, ... With one-shot workgroups every
+// CU finishes its tile at the same moment and writes it while its MFMAs idle;
+// here the next tile's first two stages are already loading while the
+// current tile is written out, and the stores drain during the next tile's
+// first K step. The C tile goes through a separate 32 KB LDS area (8 KB, 32
+// rows, per wave and pass), so the stage buffers are free for the next tile.
+// Preconditions: M % 256 == 0, N % 256 == 0, K % 64 == 0, beta == 0, C 16-byte
+// aligned, M*K*2 and N*K*2 below 2^32. Every store is then unconditional, which
+// keeps the per-wave count of outstanding vector-memory operations exact.
+template <typename T, int GA, int GB, int EPI>
+__global__ void __launch_bounds__(256, 1)
+gemm_nt_persist_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
+                       uint16_t* __restrict__ C, int M, int N, int K, float alpha,
+                       const float* __restrict__ bias, int tiles_m, int tiles_n, int group_m) {
+    constexpr int BK = 64, CH = 8, NT = 256;
+    constexpr int ROWS_PER_LOAD = kWave / CH;
+    constexpr int LOADS = kD_BM * CH / NT;
+    constexpr uint32_t STAGE_BYTES = kD_BM * BK * 2;
+    constexpr int STAGE_ROWS = 32;                     // C rows per wave and pass
+    constexpr int NSTORE = (128 / STAGE_ROWS) * (STAGE_ROWS / 4);  // 16-byte stores per lane per tile
+    static_assert(2 * LOADS + NSTORE <= 48 && NSTORE == 32, "vmcnt accounting below assumes 16 loads per stage, 32 stores");
+    __shared__ __attribute__((aligned(1024))) uint16_t smem[2 * (kD_BM + kD_BN) * BK + 4 * STAGE_ROWS * 128];
+    uint16_t* const As = smem;
+    uint16_t* const Bs = smem + 2 * kD_BM * BK;
+    uint16_t* const Cs = smem + 2 * (kD_BM + kD_BN) * BK;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave >> 1;
+    const int wn = wave & 1;
+    const int lrow = lane & 15;
+    const int lgrp = lane >> 4;
+    const int ntiles = tiles_m * tiles_n;
+    const int ktiles = K / BK;
+
+    auto tile_origin = [&](int t, int& m0, int& n0) {
+        int bid = t;
+        if ((ntiles & 7) == 0) bid = (t & 7) * (ntiles >> 3) + (t >> 3);
+        const int span = group_m * tiles_n;
+        const int grp = bid / span;
+        const int first_m = grp * group_m;
+        const int gsz = min(tiles_m - first_m, group_m);
+        const int in = bid - grp * span;
+        m0 = (first_m + in % gsz) * kD_BM;
+        n0 = (in / gsz) * kD_BN;
+    };
+
+    const uint32_t as_base = (uint32_t)(uintptr_t)&As[0];
+    const uint32_t bs_base = (uint32_t)(uintptr_t)&Bs[0];
+    const i32x4 a_rsrc = make_buf_rsrc(A, (uint32_t)((size_t)M * K * 2));
+    const i32x4 b_rsrc = make_buf_rsrc(B, (uint32_t)((size_t)N * K * 2));
+    uint32_t voff[2 * LOADS];
+    uint32_t ldso[2 * LOADS];
+    auto set_tile = [&](int m0, int n0) {
+#pragma unroll
+        for (int j = 0; j < LOADS; ++j) {
+            const int row = (j * 4 + wave) * ROWS_PER_LOAD + lane / CH;
+            const int lch = d_swz(row, lane % CH);
+            voff[j] = (uint32_t)(((size_t)(m0 + row) * K + lch * 8) * 2);
+            voff[LOADS + j] = (uint32_t)(((size_t)(n0 + row) * K + lch * 8) * 2);
+        }
+    };
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+        const uint32_t off = (uint32_t)((j * 4 + wave) * ROWS_PER_LOAD * BK * 2);
+        ldso[j] = __builtin_amdgcn_readfirstlane(as_base + off);
+        ldso[LOADS + j] = __builtin_amdgcn_readfirstlane(bs_base + off);
+    }
+    auto dma = [&](int j, int kt, int buf) {
+        lds_dma_buf_b128(j < LOADS ? a_rsrc : b_rsrc, voff[j], (uint32_t)(kt * BK * 2),
+                         ldso[j] + (uint32_t)buf * STAGE_BYTES);
+    };
+    auto issue_prologue = [&]() {
+#pragma unroll
+        for (int j = 0; j < 2 * LOADS; ++j) dma(j, 0, 0);
+#pragma unroll
+        for (int j = 0; j < 2 * LOADS; ++j) dma(j, min(1, ktiles - 1), 1);
+    };
+
+    const uint16_t* a_rd[2];
+    const uint16_t* b_rd[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int pc = (h * 4 + lgrp) ^ (lrow & 7);
+        a_rd[h] = As + (wm * 128 + lrow) * BK + pc * 8;
+        b_rd[h] = Bs + (wn * 128 + lrow) * BK + pc * 8;
+    }
+
+    f32x4 acc[8][8];
+    u32x4 fa[2][8], fb[2][8];
+    constexpr bool has_bias = (EPI & 1) != 0;  // bias != nullptr when set
+    constexpr bool relu = (EPI & 2) != 0;
+    uint16_t* const stage = Cs + wave * (STAGE_ROWS * 128);
+
+    int t = blockIdx.x;
+    int m0, n0;
+    tile_origin(t, m0, n0);
+    set_tile(m0, n0);
+    issue_prologue();
+    bool stores_pending = false;  // the previous tile's NSTORE stores follow this tile's prologue loads
+
+    for (;;) {
+        // stage 0 landed (stage 1 and the previous tile's stores may be in flight)
+        if (stores_pending) wait_vmem_le<2 * LOADS + NSTORE>();
+        else wait_vmem_le<2 * LOADS>();
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            fa[0][i] = *reinterpret_cast<const u32x4*>(a_rd[0] + i * 16 * BK);
+            fb[0][i] = *reinterpret_cast<const u32x4*>(b_rd[0] + i * 16 * BK);
+        }
 #pragma unroll
         for (int i = 0; i < 8; ++i)
 #pragma unroll
-            for (int j = 0; j < FN; ++j) acc[i][j] = mfma16x16x32(af[i], bfr[j], acc[i][j], T{});
-    };
+            for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    if constexpr (XPREFETCH) {
-        // Two fragment sets in flight: the barrier sits between the MFMAs of
-        // the two k-halves of a tile, and the first fragments of the next tile
-        // are read while the second half's MFMAs run.
-        static_assert(BK == 64 && STAGES == 2, "cross-tile prefetch is written for BK=64, 2 stages");
-        u32x4 fa[8], fb[FN], ga[8], gb[FN];
-        issue(0, 0);
-        wait_vmem_le<0>();
-        __syncthreads();
-        if (ktiles > 1) issue(1, 1);
-        read_frags(0, 0, fa, fb);
+        // K loop: same step schedule as gemm_nt_lds4k64_kernel
         for (int kt = 0; kt < ktiles; ++kt) {
-            const int buf = kt & 1;
-            read_frags(buf, 1, ga, gb);
-            mfma_block(fa, fb);
-            if (kt + 1 < ktiles) {
-                wait_vmem_le<0>();  // tile kt+1 (the only loads in flight) has landed
-                __syncthreads();    // ... for every wave; every wave finished reading buf
-                if (kt + 2 < ktiles) issue(kt + 2, buf);
-                read_frags(buf ^ 1, 0, fa, fb);
-            }
-            mfma_block(ga, gb);
-        }
-    } else {
+            const uint32_t cur = (uint32_t)(kt & 1) * (kD_BM * BK);
+            const uint32_t nxt = (uint32_t)((kt + 1) & 1) * (kD_BM * BK);
+            const int dkt = min(kt + 2, ktiles - 1);
+            const int dbuf = kt & 1;
 #pragma unroll
-        for (int s = 0; s < STAGES - 1; ++s)
-            if (s < ktiles) issue(s, s);
-        for (int kt = 0; kt < ktiles; ++kt) {
-            const int buf = kt % STAGES;
-            // stage kt must have landed; the STAGES-2 stages issued after it may stay in flight
-            if (kt + STAGES - 2 < ktiles) {
-                wait_vmem_le<(STAGES - 2) * LPT>();
-            } else {
-                wait_vmem_le<0>();
-            }
-            __syncthreads();  // all waves' data of stage kt visible; stage kt-1's buffer free
-            if (kt + STAGES - 1 < ktiles) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
+            for (int g = 0; g < 64; ++g) {
+                if (g == GA) {
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                    __syncthreads();
+                }
+                if (g == GB) {
+                    // own loads of kt+1 landed; only the 16 of kt+2 may remain
+                    // (older stores of the previous tile are complete as well)
+                    wait_vmem_le<2 * LOADS>();
+                    __syncthreads();
+                }
 #pragma unroll
-            for (int kk = 0; kk < BK / 32; ++kk) {
-                u32x4 af[8], bfr[FN];
-                read_frags(buf, kk, af, bfr);
-                mfma_block(af, bfr);
+                for (int u = 0; u < 2; ++u) {
+                    const int m = (g & 31) * 2 + u;
+                    const int i = m >> 3, j = m & 7;
+                    if (g < 32) acc[i][j] = mfma16x16x32(fb[0][j], fa[0][i], acc[i][j], T{});
+                    else acc[i][j] = mfma16x16x32(fb[1][j], fa[1][i], acc[i][j], T{});
+                }
+                if (g < 16) {
+                    const int f = g >> 1;
+                    if ((g & 1) == 0) fa[1][f] = *reinterpret_cast<const u32x4*>(a_rd[1] + cur + f * 16 * BK);
+                    else fb[1][f] = *reinterpret_cast<const u32x4*>(b_rd[1] + cur + f * 16 * BK);
+                }
+                if (g >= GA && g < GA + 16) dma(g - GA, dkt, dbuf);
+                if (g >= GB && g < GB + 16) {
+                    const int f = (g - GB) >> 1;
+                    if (((g - GB) & 1) == 0)
+                        fa[0][f] = *reinterpret_cast<const u32x4*>(a_rd[0] + nxt + f * 16 * BK);
+                    else
+                        fb[0][f] = *reinterpret_cast<const u32x4*>(b_rd[0] + nxt + f * 16 * BK);
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
-    }
+        wait_vmem_le<0>();  // all DMA writes of this tile landed ...
+        __syncthreads();    // ... for every wave; stage buffers are free
 
-    // epilogue: lane holds rows 4*(lane/16)+r, column lane%16 of each 16x16 fragment
-    const bool has_bias = (epi & 1) && bias != nullptr;
-    const bool relu = (epi & 2) != 0;
+        // bias of this lane's 32 columns, read before any new load is in flight
+        float4 bv[8];
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-        const int gn = n0 + wn * TN + j * 16 + lrow;
-        if (gn >= N) continue;
-        const float bv = has_bias ? bias[gn] : 0.f;
+        for (int j = 0; j < 8; ++j)
+            bv[j] = has_bias ? *reinterpret_cast<const float4*>(bias + n0 + wn * 128 + 16 * j + 4 * lgrp)
+                             : float4{0.f, 0.f, 0.f, 0.f};
+
+        const int cm0 = m0, cn0 = n0;
+        const int tn = t + gridDim.x;
+        const bool more = tn < ntiles;
+        if (more) {
+            tile_origin(tn, m0, n0);
+            set_tile(m0, n0);
+            issue_prologue();
+        }
+
+        // write the tile: 4 passes of 32 rows per wave through the LDS stage
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int pass = 0; pass < 128 / STAGE_ROWS; ++pass) {
+            // Keep at most 48 vector-memory operations outstanding (the counter
+            // holds 63): before the last two passes' stores, wait for the next
+            // tile's stage 0 (the oldest 16 of 32 loads + 16 stores).
+            if (pass == 2 && more) wait_vmem_le<4 * LOADS>();
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int gm = m0 + wm * 128 + i * 16 + lgrp * 4 + r;
-                if (gm >= M) continue;
-                float v = alpha * acc[i][j][r];
-                uint16_t* cp = C + (size_t)gm * N + gn;
-                if (beta != 0.f) v += beta * elem<T>::to_f32(*cp);
-                v += bv;
-                if (relu) v = v > 0.f ? v : 0.f;
-                *cp = elem<T>::from_f32(v);
+            for (int j = 0; j < 8; ++j) {
+                const int c = 16 * j + 4 * lgrp;
+#pragma unroll
+                for (int ii = 0; ii < STAGE_ROWS / 16; ++ii) {
+                    const int i = pass * (STAGE_ROWS / 16) + ii;
+                    const int r = 16 * ii + lrow;
+                    float v[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        v[e] = alpha * acc[i][j][e];
+                        if (has_bias) v[e] += (&bv[j].x)[e];
+                        if (relu) v[e] = fmaxf(v[e], 0.f);
+                    }
+                    uint2 packed;
+                    packed.x = (uint32_t)elem<T>::from_f32(v[0]) | ((uint32_t)elem<T>::from_f32(v[1]) << 16);
+                    packed.y = (uint32_t)elem<T>::from_f32(v[2]) | ((uint32_t)elem<T>::from_f32(v[3]) << 16);
+                    *reinterpret_cast<uint2*>(stage + r * 128 + (((c >> 3) ^ (r & 15)) << 3) + (c & 4)) = packed;
+                }
+            }
+#pragma unroll
+            for (int p = 0; p < STAGE_ROWS / 4; ++p) {
+                const int r = 4 * p + lgrp;
+                const uint4 val = *reinterpret_cast<const uint4*>(stage + r * 128 + ((lrow ^ (r & 15)) << 3));
+                const int gm = cm0 + wm * 128 + pass * STAGE_ROWS + r;
+                *reinterpret_cast<uint4*>(C + (size_t)gm * N + cn0 + wn * 128 + lrow * 8) = val;
             }
         }
+        if (!more) break;
+        t = tn;
+        stores_pending = true;
     }
+    wait_vmem_le<0>();
 }
 
 }  // namespace pyc
 
-// Returns 1 when the shape is outside this kernel's preconditions (caller
-// uses another variant), 0 on launch, -2 on a launch error.
-// PYC_GEMM_LDS_CFG selects the pipeline shape for tuning: 3 = 8 waves, BK64 x 2
-// stages with cross-tile fragment prefetch (default), 1 = 8 waves, BK64 x 2,
-// 0 = 8 waves, BK32 x 4, 2 = 8 waves, BK32 x 5, 4 = 4 waves of 128x128 with
-// fragment prefetch, 5 = 4 waves of 128x128 plain.
+// Returns 1 when the shape is outside these kernels' preconditions (the caller
+// uses another variant), 0 on launch, -2 on a launch error. Full-tile shapes
+// with beta == 0 take the persistent kernel; PYC_GEMM_NT_PERSIST=0 forces the
+// one-shot kernel (for comparisons).
 extern "C" int pyc_hip_gemm_nt_lds_launch(int is_bf16, int M, int N, int K, const void* A, const void* B,
                                           void* C, float alpha, float beta, const float* bias, int epi,
                                           void* stream) {
     using namespace pyc;
-    static int cfg = -1;
-    if (cfg < 0) {
-        const char* e = getenv("PYC_GEMM_LDS_CFG");
-        cfg = e ? atoi(e) : 3;
+    if (M <= 0 || N <= 0 || K <= 0 || K % 64 != 0) return 1;
+    // buffer descriptors hold 32-bit byte counts
+    if ((size_t)M * K * 2 > 0xFFFFFFFFull || (size_t)N * K * 2 > 0xFFFFFFFFull) return 1;
+    static int persist_env = -1;
+    static int n_cu = 0;
+    if (persist_env < 0) {
+        const char* e = getenv("PYC_GEMM_NT_PERSIST");
+        persist_env = (e && e[0] == '0') ? 0 : 1;
     }
-    const int bk = (cfg == 0 || cfg == 2) ? 32 : 64;
-    if (K % bk != 0 || M <= 0 || N <= 0) return 1;
+    if (n_cu == 0) {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
+            n_cu = cus;
+        else
+            n_cu = 256;
+    }
     const int tiles_m = (M + kD_BM - 1) / kD_BM;
     const int tiles_n = (N + kD_BN - 1) / kD_BN;
-    const int waves = (cfg >= 4) ? 4 : 8;
-    dim3 grid(tiles_m * tiles_n), block(waves * kWave);
+    const int ntiles = tiles_m * tiles_n;
+    const bool persist = persist_env && M % kD_BM == 0 && N % kD_BN == 0 && beta == 0.f &&
+                         ((uintptr_t)C & 15) == 0 && ((epi & 1) == 0 || bias == nullptr || ((uintptr_t)bias & 15) == 0);
     hipStream_t s = (hipStream_t)stream;
-#define PYC_LDS_LAUNCH(TY, BK_, ST_, XP_, W_)                                                          \
-    hipLaunchKernelGGL((gemm_nt_lds_kernel<TY, BK_, ST_, XP_, W_>), grid, block, 0, s, (const uint16_t*)A, \
-                       (const uint16_t*)B, (uint16_t*)C, M, N, K, alpha, beta, bias, epi, tiles_m, tiles_n, 8)
-    if (is_bf16) {
-        if (cfg == 1) PYC_LDS_LAUNCH(bf16_t, 64, 2, false, 8);
-        else if (cfg == 2) PYC_LDS_LAUNCH(bf16_t, 32, 5, false, 8);
-        else if (cfg == 0) PYC_LDS_LAUNCH(bf16_t, 32, 4, false, 8);
-        else if (cfg == 4) PYC_LDS_LAUNCH(bf16_t, 64, 2, true, 4);
-        else if (cfg == 5) PYC_LDS_LAUNCH(bf16_t, 64, 2, false, 4);
-        else PYC_LDS_LAUNCH(bf16_t, 64, 2, true, 8);
+    const dim3 block(4 * kWave);
+    const uint16_t* a = (const uint16_t*)A;
+    const uint16_t* b = (const uint16_t*)B;
+    uint16_t* c = (uint16_t*)C;
+    if (persist) {
+        const int pepi = (((epi & 1) && bias != nullptr) ? 1 : 0) | (epi & 2);
+        const dim3 grid(ntiles < n_cu ? ntiles : n_cu);
+#define PYC_PERSIST(TY, E) \
+    hipLaunchKernelGGL((gemm_nt_persist_kernel<TY, 24, 40, E>), grid, block, 0, s, a, b, c, M, N, K, alpha, bias, \
+                       tiles_m, tiles_n, 8)
+        if (is_bf16) {
+            if (pepi == 0) PYC_PERSIST(bf16_t, 0);
+            else if (pepi == 1) PYC_PERSIST(bf16_t, 1);
+            else if (pepi == 2) PYC_PERSIST(bf16_t, 2);
+            else PYC_PERSIST(bf16_t, 3);
+        } else {
+            if (pepi == 0) PYC_PERSIST(f16_t, 0);
+            else if (pepi == 1) PYC_PERSIST(f16_t, 1);
+            else if (pepi == 2) PYC_PERSIST(f16_t, 2);
+            else PYC_PERSIST(f16_t, 3);
+        }
+#undef PYC_PERSIST
     } else {
-        if (cfg == 1) PYC_LDS_LAUNCH(f16_t, 64, 2, false, 8);
-        else if (cfg == 2) PYC_LDS_LAUNCH(f16_t, 32, 5, false, 8);
-        else if (cfg == 0) PYC_LDS_LAUNCH(f16_t, 32, 4, false, 8);
-        else if (cfg == 4) PYC_LDS_LAUNCH(f16_t, 64, 2, true, 4);
-        else if (cfg == 5) PYC_LDS_LAUNCH(f16_t, 64, 2, false, 4);
-        else PYC_LDS_LAUNCH(f16_t, 64, 2, true, 8);
+        const dim3 grid(ntiles);
+        if (is_bf16)
+            hipLaunchKernelGGL((gemm_nt_lds4k64_kernel<bf16_t, 24, 40>), grid, block, 0, s, a, b, c, M, N, K, alpha,
+                               beta, bias, epi, tiles_m, tiles_n, 8);
+        else
+            hipLaunchKernelGGL((gemm_nt_lds4k64_kernel<f16_t, 24, 40>), grid, block, 0, s, a, b, c, M, N, K, alpha,
+                               beta, bias, epi, tiles_m, tiles_n, 8);
     }
-#undef PYC_LDS_LAUNCH
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }

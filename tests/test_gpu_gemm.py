@@ -42,10 +42,10 @@ SHAPES = [(256, 256, 64), (512, 768, 256), (300, 200, 72), (1, 1, 8), (33, 65, 4
 
 @pytest.mark.parametrize("m,n,k", SHAPES)
 @pytest.mark.parametrize("layout", ["nt", "nn"])
-@pytest.mark.parametrize("tile", ["", "_128x128", "_256x256", "_256x256_lds8"])
+@pytest.mark.parametrize("tile", ["", "_128x128", "_256x256", "_256x256_lds"])
 def test_bf16_gemm_vs_oracle(gpu, m, n, k, layout, tile):
     torch = gpu
-    if tile.endswith("lds8") and layout == "nn":
+    if tile.endswith("lds") and layout == "nn":
         pytest.skip("the direct-LDS kernel is NT only")
     bt = layout == "nt"
     a, b = _bf16_inputs(m, n, k, m * 7 + n + k, bt)
@@ -77,6 +77,56 @@ def test_bf16_gemm_8192_sampled_rows(gpu):
     colsum = Cd.float().sum(0).double()
     pred = (A.double().sum(0, keepdim=True) @ B.double().t()).squeeze(0)
     assert (colsum - pred).abs().max().item() <= 1e-2 * pred.abs().max().item()
+
+
+def test_bf16_nt_lds_more_tiles_than_cus(gpu):
+    """17 x 17 tiles of 256 x 256 on 256 CUs: the persistent direct-LDS kernel
+    runs two tiles on some workgroups (next tile's loads overlap the previous
+    tile's stores). Every element is checked."""
+    torch = gpu
+    m = n = 17 * 256
+    k = 128
+    a, b = _bf16_inputs(m, n, k, 17, True)
+    A, B = dev_bits16(torch, a), dev_bits16(torch, b)
+    Cd = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    pyc_amd.gemm("hip_gemm_bf16_nt_256x256_lds", A, B, Cd, m, n, k)
+    torch.cuda.synchronize()
+    _check_half(host_bits16(Cd), oracle.gemm_bf16(a, b, True, threads=8), k)
+
+
+@pytest.mark.parametrize("alpha,beta,epi", [(0.5, 0.0, 3), (1.0, 0.0, 2), (-2.0, 0.0, 1), (0.75, 0.5, 3)])
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_nt_lds_epilogues_full_tiles(gpu, alpha, beta, epi, dtype):
+    """Whole 256 x 256 tiles: beta == 0 takes the persistent kernel (bias /
+    ReLU compiled in), beta != 0 the one-shot kernel that reads C back."""
+    torch = gpu
+    m, n, k = 512, 768, 256
+    r = np.random.default_rng(abs(int(alpha * 100)) + epi)
+    a32 = (r.standard_normal((m, k)) / np.sqrt(k)).astype(np.float32)
+    b32 = r.standard_normal((n, k)).astype(np.float32)
+    c32 = r.standard_normal((m, n)).astype(np.float32)
+    bias = r.standard_normal(n).astype(np.float32)
+    if dtype == "bf16":
+        a, b, c0 = oracle.f32_to_bf16(a32), oracle.f32_to_bf16(b32), oracle.f32_to_bf16(c32)
+        A, B, Cd = dev_bits16(torch, a), dev_bits16(torch, b), dev_bits16(torch, c0.copy())
+        prod, cin = oracle.gemm_bf16(a, b, True), oracle.bf16_to_f32(c0)
+    else:
+        a, b, c0 = a32.astype(np.float16), b32.astype(np.float16), c32.astype(np.float16)
+        A, B, Cd = (torch.from_numpy(x.copy()).cuda() for x in (a, b, c0))
+        prod = oracle.matmul_f32(a.astype(np.float32), np.ascontiguousarray(b.astype(np.float32).T))
+        cin = c0.astype(np.float32)
+    pyc_amd.gemm(f"hip_gemm_{dtype}_nt_256x256_lds", A, B, Cd, m, n, k, alpha=alpha, beta=beta,
+                 bias=dev_f32(torch, bias) if epi & 1 else None, epilogue=epi)
+    torch.cuda.synchronize()
+    ref = alpha * prod + beta * cin + (bias if epi & 1 else 0.0)
+    if epi & 2:
+        ref = np.maximum(ref, 0.0)
+    if dtype == "bf16":
+        _check_half(host_bits16(Cd), ref, k)
+    else:
+        got = Cd.float().cpu().numpy()
+        assert rel_max_err(got, ref) <= BF16_TOL
+        assert np.all(np.abs(got - ref) <= 2.0 ** -10 * np.abs(ref) + 1e-5 * np.sqrt(k) * np.abs(ref).max())
 
 
 @pytest.mark.parametrize("layout", ["nt", "nn"])
