@@ -44,6 +44,9 @@
 #include "pyc/kernel_registry.h"
 #include "pyc_mutex.h"
 
+/* split-K workspace of the fp8 GEMM (gemm_w8a16.hip); allocates outside capture */
+int pyc_hip_w8a16_reserve(int N, int K);
+
 static pyc_mutex g_dispatch_lock = PYC_MUTEX_INIT;
 
 /* ---------------------------------------------------------------- env */
@@ -927,6 +930,12 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
             g_ws.graph_valid = 0;
         }
         if (use_graph) {
+            /* the fp8 GEMM's split-K workspace cannot be allocated inside a capture */
+            for (i = 0; i < plan.nsteps; ++i) {
+                if (plan.steps[i].kind == ST_W8A16) {
+                    (void)pyc_hip_w8a16_reserve(plan.steps[i].n, plan.steps[i].k);
+                }
+            }
             cerr = hipStreamBeginCapture(g_ws.stream, hipStreamCaptureModeThreadLocal);
         }
         if (cerr == hipSuccess) {

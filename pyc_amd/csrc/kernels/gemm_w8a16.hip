@@ -16,14 +16,29 @@
 // bytes 0-7 feed MFMA #1 and bytes 8-15 MFMA #2, and the X fragments are read
 // at exactly those k, so both operands use the same k permutation.
 //
-// Workgroup = 4 waves over 16*NR_TILES output channels; wave w walks the 64-k
-// steps s = w, w+4, ... and the four partial sums are reduced through LDS.
+// Work split ("stream-K"): an item is 64 output channels x 64 k. The
+// N/64 x K/64 items are cut into one contiguous run per workgroup, one
+// workgroup per CU, so every CU streams the same number of weight bytes even
+// when N/64 is far below the CU count (N = 4096 gives 64 channel units). 64
+// channels per unit make the activation bytes a workgroup reads equal to its
+// weight bytes (32 tokens x 2 bytes vs 64 channels x 1 byte per k).
+// Inside a workgroup the 8 waves take every 8th item of a unit's run, keep
+// two items' loads in flight, and reduce through LDS. A unit whose k range is
+// split over several workgroups is finished by the last of them to arrive:
+// each writes its fp32 partial to a workspace slot with agent-scope stores,
+// waits for them to complete, then bumps the unit's counter; the one that
+// sees the final count reads the slots with agent-scope loads, applies
+// scale/ReLU, writes Y and resets the counter to zero for the next launch (so
+// graph replays need no memset).
+// Without a workspace every workgroup owns whole units instead.
 #include "common.hpp"
+#include "lds_dma.hpp"
 
 namespace pyc {
 
-constexpr int kW8Waves = 4;
-constexpr int kW8Tiles = 2;  // 16-row weight tiles per workgroup (32 channels)
+constexpr int kW8Waves = 8;
+constexpr int kW8Rows = 64;  // output channels per unit: 4 MFMA row blocks
+constexpr int kW8K = 64;     // k per item
 
 __device__ inline u32x4 fp8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
     // Two fp8 per conversion; fp32 -> bf16 by truncation is exact here.
@@ -40,87 +55,584 @@ __device__ inline u32x4 fp8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
     return r;
 }
 
-__global__ void __launch_bounds__(kW8Waves * kWave)
-w8a16_kernel(const uint16_t* __restrict__ X, const uint8_t* __restrict__ Wq,
-             const float* __restrict__ scale, uint16_t* __restrict__ Y, int M, int N, int K,
-             int relu) {
-    __shared__ f32x4 red[kW8Waves][kW8Tiles][2][kWave];
+// Operands of one item for one wave: 4 weight row blocks (16 rows x 64 k of
+// fp8, one 16-byte load per lane each) and the two 16-token halves of X
+// (two 16-byte loads per lane each). Every load is issued unconditionally
+// from a clamped, in-bounds address; lanes outside K or M are zeroed after the
+// load. Branch-free loads let the compiler count outstanding loads exactly
+// (s_waitcnt vmcnt(n) for the oldest item) instead of draining all of them.
+struct W8Item {
+    u32x4 w[4];
+    u32x4 x[2][2];
+};
 
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+__device__ inline void w8_load(W8Item& f, const uint16_t* __restrict__ X, const uint8_t* __restrict__ Wq, int M,
+                               int N, int K, int unit, int step, int lane) {
     const int lrow = lane & 15;
-    const int g = lane >> 4;
-    const int nbase = blockIdx.x * (16 * kW8Tiles);
-    const int steps = (K + 63) / 64;
-
-    f32x4 acc[kW8Tiles][2];
+    const int k = min(step * kW8K + (lane >> 4) * 16, K - 16);  // K % 16 == 0
 #pragma unroll
-    for (int t = 0; t < kW8Tiles; ++t)
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) acc[t][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    const int m0 = lrow;
-    const int m1 = 16 + lrow;
-    for (int s = wave; s < steps; s += kW8Waves) {
-        // K % 16 == 0: a lane's 16 k are all in range or all out (tail step);
-        // out-of-range lanes feed zeros so control flow stays uniform around the MFMAs.
-        const int k = s * 64 + g * 16;
-        const bool kin = k < K;
-        u32x4 xf[2][2];
-        xf[0][0] = (kin && m0 < M) ? *reinterpret_cast<const u32x4*>(X + (size_t)m0 * K + k) : u32x4{0, 0, 0, 0};
-        xf[0][1] = (kin && m0 < M) ? *reinterpret_cast<const u32x4*>(X + (size_t)m0 * K + k + 8) : u32x4{0, 0, 0, 0};
-        xf[1][0] = (kin && m1 < M) ? *reinterpret_cast<const u32x4*>(X + (size_t)m1 * K + k) : u32x4{0, 0, 0, 0};
-        xf[1][1] = (kin && m1 < M) ? *reinterpret_cast<const u32x4*>(X + (size_t)m1 * K + k + 8) : u32x4{0, 0, 0, 0};
-#pragma unroll
-        for (int t = 0; t < kW8Tiles; ++t) {
-            const int n = nbase + t * 16 + lrow;
-            u32x4 wv = u32x4{0, 0, 0, 0};
-            if (kin && n < N) wv = *reinterpret_cast<const u32x4*>(Wq + (size_t)n * K + k);
-            const u32x4 w0 = fp8x8_to_bf16x8(wv[0], wv[1]);
-            const u32x4 w1 = fp8x8_to_bf16x8(wv[2], wv[3]);
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt) {
-                acc[t][mt] = mfma16x16x32(w0, xf[mt][0], acc[t][mt], bf16_t{});
-                acc[t][mt] = mfma16x16x32(w1, xf[mt][1], acc[t][mt], bf16_t{});
-            }
-        }
+    for (int rb = 0; rb < 4; ++rb) {
+        const int n = min(unit * kW8Rows + rb * 16 + lrow, N - 1);
+        f.w[rb] = *reinterpret_cast<const u32x4*>(Wq + (size_t)n * K + k);
     }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int t = min(h * 16 + lrow, M - 1);
+        f.x[h][0] = *reinterpret_cast<const u32x4*>(X + (size_t)t * K + k);
+        f.x[h][1] = *reinterpret_cast<const u32x4*>(X + (size_t)t * K + k + 8);
+    }
+}
 
+// Zeroes the X fragments of lanes whose k lies past K or whose token is past
+// M, and all of them when the item is not `live` (their weight bytes then
+// multiply zeros).
+__device__ inline void w8_mask(W8Item& f, int M, int K, int step, bool live, int lane) {
+    const bool kin = live && step * kW8K + (lane >> 4) * 16 < K;
 #pragma unroll
-    for (int t = 0; t < kW8Tiles; ++t)
+    for (int h = 0; h < 2; ++h) {
+        const bool ok = kin && h * 16 + (lane & 15) < M;
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) red[wave][t][mt][lane] = acc[t][mt];
-    __syncthreads();
-    if (wave != 0) return;
+        for (int q = 0; q < 2; ++q)
 #pragma unroll
-    for (int t = 0; t < kW8Tiles; ++t) {
+            for (int c = 0; c < 4; ++c) f.x[h][q][c] = ok ? f.x[h][q][c] : 0u;
+    }
+}
+
+__device__ inline void w8_mma(f32x4 (&acc)[4][2], const W8Item& f) {
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-            f32x4 v = red[0][t][mt][lane];
+    for (int rb = 0; rb < 4; ++rb) {
+        const u32x4 w0 = fp8x8_to_bf16x8(f.w[rb][0], f.w[rb][1]);
+        const u32x4 w1 = fp8x8_to_bf16x8(f.w[rb][2], f.w[rb][3]);
 #pragma unroll
-            for (int w = 1; w < kW8Waves; ++w) v += red[w][t][mt][lane];
-            // lane holds D[n = 4*g + r][m = lrow] of the (t, mt) tile
-            const int m = mt * 16 + lrow;
-            if (m >= M) continue;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int n = nbase + t * 16 + g * 4 + r;
-                if (n >= N) continue;
-                float y = v[r] * scale[n];
-                if (relu) y = y > 0.f ? y : 0.f;
-                Y[(size_t)m * N + n] = elem<bf16_t>::from_f32(y);
-            }
+        for (int h = 0; h < 2; ++h) {
+            acc[rb][h] = mfma16x16x32(w0, f.x[h][0], acc[rb][h], bf16_t{});
+            acc[rb][h] = mfma16x16x32(w1, f.x[h][1], acc[rb][h], bf16_t{});
         }
     }
 }
 
+// 16-byte accesses that are coherent across the XCDs' L2 caches (sc1, the
+// policy the compiler uses for agent-scope atomic loads and stores), for the
+// split-K partials. The caller waits (s_waitcnt vmcnt) before relying on them:
+// these are asm, so the compiler does not track them.
+__device__ inline void store_coherent_b128(float* p, const f32x4& v) {
+    asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+}
+__device__ inline f32x4 load_coherent_b128(const float* p) {
+    f32x4 v;
+    asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(v) : "v"(p) : "memory");
+    return v;
+}
+
+// Workgroup that owns item i under an even split of `total` items over G
+// workgroups (the first `rem` get base + 1 items).
+__device__ __host__ inline int w8_owner(int i, int base, int rem) {
+    const int cut = rem * (base + 1);
+    return i < cut ? i / (base + 1) : rem + (i - cut) / base;
+}
+
+__global__ void __launch_bounds__(kW8Waves * kWave)
+w8a16_kernel(const uint16_t* __restrict__ X, const uint8_t* __restrict__ Wq, const float* __restrict__ scale,
+             uint16_t* __restrict__ Y, int M, int N, int K, int relu, int base, int rem, float* __restrict__ part,
+             int* __restrict__ cnt, int max_slots) {
+    __shared__ f32x4 red[kW8Waves][4][2][kWave];
+    __shared__ int s_last;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: loop bounds stay scalar
+    const int ksteps = (K + kW8K - 1) / kW8K;
+    const int g = blockIdx.x;
+    int i = g * base + min(g, rem);
+    const int i1 = i + base + (g < rem ? 1 : 0);
+
+    while (i < i1) {
+        const int unit = i / ksteps;
+        const int ka = i - unit * ksteps;
+        const int kb = min(ksteps, ka + (i1 - i));
+
+        f32x4 acc[4][2];
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) acc[rb][h] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+        // This wave's items: ka + wave + 8j, j < nj; three in flight. The loop
+        // body always consumes three items and always issues three loads:
+        // positions past the last item re-read it (an L2 hit) and are zeroed
+        // before their MFMAs. With no early exit, every load has a use on all
+        // paths, so the compiler keeps it where it is written (ahead of its
+        // use) and can wait on exact outstanding-load counts.
+        const int nj = max(0, (kb - ka - wave + kW8Waves - 1) / kW8Waves);
+        const int slast = ka + wave + kW8Waves * max(nj - 1, 0);
+        auto item = [&](int j) { return min(ka + wave + kW8Waves * j, slast); };
+        if (nj > 0) {
+            W8Item f0, f1, f2;
+            w8_load(f0, X, Wq, M, N, K, unit, item(0), lane);
+            w8_load(f1, X, Wq, M, N, K, unit, item(1), lane);
+            w8_load(f2, X, Wq, M, N, K, unit, item(2), lane);
+            // sched_barrier keeps each refill after the MFMAs that free its
+            // registers and ahead of the next item's MFMAs
+            for (int j = 0; j < nj; j += 3) {
+                w8_mask(f0, M, K, item(j), true, lane);
+                w8_mma(acc, f0);
+                __builtin_amdgcn_sched_barrier(0);
+                w8_load(f0, X, Wq, M, N, K, unit, item(j + 3), lane);
+                __builtin_amdgcn_sched_barrier(0);
+                w8_mask(f1, M, K, item(j + 1), j + 1 < nj, lane);
+                w8_mma(acc, f1);
+                __builtin_amdgcn_sched_barrier(0);
+                w8_load(f1, X, Wq, M, N, K, unit, item(j + 4), lane);
+                __builtin_amdgcn_sched_barrier(0);
+                w8_mask(f2, M, K, item(j + 2), j + 2 < nj, lane);
+                w8_mma(acc, f2);
+                __builtin_amdgcn_sched_barrier(0);
+                w8_load(f2, X, Wq, M, N, K, unit, item(j + 5), lane);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) red[wave][rb][h][lane] = acc[rb][h];
+        __syncthreads();
+        // thread tid owns entry (rb, h, lane) = (tid >> 7, (tid >> 6) & 1, tid & 63)
+        const int rb = tid >> 7;
+        const int h = (tid >> 6) & 1;
+        f32x4 v = red[0][rb][h][lane];
+#pragma unroll
+        for (int w = 1; w < kW8Waves; ++w) v += red[w][rb][h][lane];
+
+        bool finish = true;
+        if (ka != 0 || kb != ksteps) {
+            // k range of this unit is shared with other workgroups
+            const int first = w8_owner(unit * ksteps, base, rem);
+            const int nslots = w8_owner(unit * ksteps + ksteps - 1, base, rem) - first + 1;
+            // Partials are written and read with agent-scope accesses (coherent
+            // across the XCDs' L2s without whole-cache write-back/invalidate,
+            // which an agent-scope fence would cost every workgroup).
+            float* slots = part + (size_t)unit * max_slots * (kW8Waves * kWave * 4);
+            float* mine = slots + ((size_t)(g - first) * (kW8Waves * kWave) + tid) * 4;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) __hip_atomic_store(mine + c, v[c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the partial has reached the coherent level
+            __syncthreads();
+            if (tid == 0) {
+                const int old = __hip_atomic_fetch_add(&cnt[unit], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                s_last = old == nslots - 1;
+                // every contributor has arrived: re-arm for the next launch (an
+                // agent-scope store writes through this XCD's L2)
+                if (s_last) __hip_atomic_store(&cnt[unit], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            __syncthreads();
+            finish = s_last != 0;
+            if (finish) {
+                v = f32x4{0.f, 0.f, 0.f, 0.f};
+                for (int sl = 0; sl < nslots; ++sl) {
+                    const float* src = slots + ((size_t)sl * (kW8Waves * kWave) + tid) * 4;
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+                        v[c] += __hip_atomic_load(src + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+        }
+        if (finish) {
+            // D layout: lane holds channel 4*(lane/16) + r of row block rb, token lane % 16 of half h
+            const int t = h * 16 + (lane & 15);
+            if (t < M) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int n = unit * kW8Rows + rb * 16 + (lane >> 4) * 4 + r;
+                    if (n < N) {
+                        float y = v[r] * scale[n];
+                        if (relu) y = y > 0.f ? y : 0.f;
+                        Y[(size_t)t * N + n] = elem<bf16_t>::from_f32(y);
+                    }
+                }
+            }
+        }
+        __syncthreads();  // red[] is rewritten by the next unit
+        i += kb - ka;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// LDS-staged form (K % 128 == 0). An item is 64 channels x 128 k: 8 KB of
+// weights (one whole 128-byte line of each row) and 8 KB of X (32 tokens x
+// 256 bytes). Register-direct fragment loads touch 16 lines per instruction
+// and use 64 bytes of each, which leaves the L1 tag path as the bottleneck;
+// here every buffer_load ... lds instruction moves whole lines (8 weight rows
+// x 128 B, or 4 tokens x 256 B) straight into LDS, and the MFMA fragments are
+// read back from XOR-swizzled LDS (16-byte chunk c of row r at c ^ (r & 7) for
+// weights, c ^ (t & 15) for X tokens, so fragment reads are conflict free).
+// A ring of kQStages items keeps 7 items (112 KB) of loads in flight per CU.
+// Wave w owns channels 16w..16w+15 of the unit for all k, so no intra-group
+// reduction is needed. The split-K finish (same protocol as the kernel above)
+// counts an arrival only after the partial's stores completed, which would
+// drain the load pipeline mid-run; since only the first and the last segment
+// of a workgroup's run can be partial, the first partial is stored when its
+// segment ends and both arrivals are counted after the last item.
+// Rows past N and tokens past M read zero through the descriptors' byte counts.
+constexpr int kQWaves = 4;
+constexpr int kQK = 128;
+constexpr int kQStages = 8;
+constexpr int kQWBytes = kW8Rows * kQK;      // weight bytes per item
+constexpr int kQXBytes = 32 * kQK * 2;       // X bytes per item (32 tokens)
+constexpr int kQStageBytes = kQWBytes + kQXBytes;
+
+__global__ void __launch_bounds__(kQWaves * kWave)
+w8a16_lds_kernel(const uint16_t* __restrict__ X, const uint8_t* __restrict__ Wq, const float* __restrict__ scale,
+                 uint16_t* __restrict__ Y, int M, int N, int K, int relu, int base, int rem,
+                 float* __restrict__ part, int* __restrict__ cnt, int max_slots) {
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[kQStages * kQStageBytes];
+    __shared__ int s_last;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kitems = K / kQK;
+    const int g = blockIdx.x;
+    const int i0 = g * base + min(g, rem);
+    const int nitems = base + (g < rem ? 1 : 0);
+
+    const i32x4 wrs = make_buf_rsrc(Wq, (uint32_t)((size_t)N * K));
+    const i32x4 xrs = make_buf_rsrc(X, (uint32_t)((size_t)M * K * 2));
+    const uint32_t lds0 = (uint32_t)(uintptr_t)&smem[0];
+
+    // DMA instruction q = 2*wave + e of an item: weight rows 8q..8q+7 (lane l:
+    // row 8q + l/8, physical chunk l%8 holding logical chunk (l%8) ^ (row&7)),
+    // X tokens 4q..4q+3 (lane l: token 4q + l/16, physical chunk l%16 holding
+    // logical chunk (l%16) ^ (token&15)).
+    int wrow[2];
+    uint32_t wcol[2], xvo[2], wlds[2], xlds[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const int q = 2 * wave + e;
+        wrow[e] = 8 * q + lane / 8;
+        wcol[e] = (uint32_t)((((lane % 8) ^ (wrow[e] & 7))) * 16);
+        const int tok = 4 * q + lane / 16;
+        xvo[e] = (uint32_t)tok * (uint32_t)K * 2u + (uint32_t)(((lane % 16) ^ (tok & 15)) * 16);
+        wlds[e] = __builtin_amdgcn_readfirstlane(lds0 + q * 1024);
+        xlds[e] = __builtin_amdgcn_readfirstlane(lds0 + kQWBytes + q * 1024);
+    }
+    auto dma = [&](int item, int stage) {
+        const int unit = item / kitems;
+        const int kk = item - unit * kitems;
+        const uint32_t sb = (uint32_t)stage * kQStageBytes;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const uint32_t wvo = (uint32_t)(unit * kW8Rows + wrow[e]) * (uint32_t)K + wcol[e];
+            lds_dma_buf_b128(wrs, wvo, (uint32_t)(kk * kQK), wlds[e] + sb);
+        }
+#pragma unroll
+        for (int e = 0; e < 2; ++e) lds_dma_buf_b128(xrs, xvo[e], (uint32_t)(kk * kQK * 2), xlds[e] + sb);
+    };
+
+    // fragment offsets within a stage
+    const int lr = lane & 15;
+    const int lg = lane >> 4;
+    const int frow = 16 * wave + lr;
+    uint32_t w_rd[2];
+    uint32_t x_rd[2][2][2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        w_rd[j] = (uint32_t)(frow * kQK + (((lg + 4 * j) ^ (frow & 7)) * 16));
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const int t = 16 * h + lr;
+                x_rd[h][j][q] = (uint32_t)(kQWBytes + t * (kQK * 2) + (((8 * j + 2 * lg + q) ^ (t & 15)) * 16));
+            }
+    }
+
+    if (nitems <= 0) return;
+    const int ilast = i0 + nitems - 1;
+#pragma unroll
+    for (int st = 0; st < kQStages - 1; ++st) dma(min(i0 + st, ilast), st);
+
+    // lane holds channels 16*wave + 4*(lane/16) + r, token 16h + lane%16
+    auto q_store_y = [&](int unit, const f32x4 (&v)[2]) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int t = 16 * h + lr;
+            if (t >= M) continue;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int nch = unit * kW8Rows + 16 * wave + 4 * lg + r;
+                if (nch < N) {
+                    float y = v[h][r] * scale[nch];
+                    if (relu) y = y > 0.f ? y : 0.f;
+                    Y[(size_t)t * N + nch] = elem<bf16_t>::from_f32(y);
+                }
+            }
+        }
+    };
+    // Units shared with other workgroups: each contributor publishes its
+    // partial to its slot, counts its arrival, and the last arrival sums all
+    // partials and writes Y. Slots and counters use agent-scope accesses.
+    auto q_slots = [&](int unit) { return part + (size_t)unit * max_slots * (kQWaves * kWave * 2 * 4); };
+    auto q_first = [&](int unit) { return w8_owner(unit * kitems, base, rem); };
+    auto q_nslots = [&](int unit) { return w8_owner(unit * kitems + kitems - 1, base, rem) - q_first(unit) + 1; };
+    auto q_publish = [&](int unit, const f32x4 (&v)[2]) {
+        float* mine = q_slots(unit) + ((size_t)(g - q_first(unit)) * (kQWaves * kWave * 2) + (size_t)tid * 2) * 4;
+        store_coherent_b128(mine, v[0]);
+        store_coherent_b128(mine + 4, v[1]);
+    };
+    // Last arrival for up to two units: every slot load of both is issued
+    // before one wait, then the sums are formed and Y is written.
+    auto q_reduce2 = [&](int u0, int u1) {
+        constexpr int kMaxSlots = 8;  // the launcher caps max_slots at this
+        f32x4 got[2][kMaxSlots][2];
+        const int ns[2] = {u0 >= 0 ? q_nslots(u0) : 0, u1 >= 0 ? q_nslots(u1) : 0};
+#pragma unroll
+        for (int uu = 0; uu < 2; ++uu) {
+            const float* slots = q_slots(uu == 0 ? u0 : u1);
+#pragma unroll
+            for (int sl = 0; sl < kMaxSlots; ++sl) {
+                if (sl < ns[uu]) {
+                    const float* src = slots + ((size_t)sl * (kQWaves * kWave * 2) + (size_t)tid * 2) * 4;
+                    got[uu][sl][0] = load_coherent_b128(src);
+                    got[uu][sl][1] = load_coherent_b128(src + 4);
+                }
+            }
+        }
+        wait_vmem_le<0>();
+#pragma unroll
+        for (int uu = 0; uu < 2; ++uu) {
+            if (ns[uu] == 0) continue;
+            f32x4 sum[2] = {got[uu][0][0], got[uu][0][1]};
+#pragma unroll
+            for (int sl = 1; sl < kMaxSlots; ++sl)
+                if (sl < ns[uu]) {
+                    sum[0] += got[uu][sl][0];
+                    sum[1] += got[uu][sl][1];
+                }
+            q_store_y(uu == 0 ? u0 : u1, sum);
+        }
+    };
+
+    int seg_start = i0;
+    int pend_unit = -1, last_unit = -1;
+
+    // Fragments of one item, read from its stage; two sets rotate so the next
+    // item's LDS reads are in flight while the current item's MFMAs run.
+    struct QFrag {
+        u32x4 w[2];
+        u32x4 x[2][2][2];
+    };
+    auto read_frag = [&](int n, QFrag& f) {
+        const uint8_t* stage = smem + (n % kQStages) * kQStageBytes;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            f.w[j] = *reinterpret_cast<const u32x4*>(stage + w_rd[j]);
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int q = 0; q < 2; ++q) f.x[h][j][q] = *reinterpret_cast<const u32x4*>(stage + x_rd[h][j][q]);
+        }
+    };
+    // Two accumulator sets (even and odd items) keep two independent MFMA
+    // chains per token half.
+    f32x4 accs[2][2];
+#pragma unroll
+    for (int a2 = 0; a2 < 2; ++a2) accs[a2][0] = accs[a2][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto process = [&](int n, const QFrag& cur, QFrag& nxt, f32x4 (&acc)[2]) {
+        // own loads of items n and n+1 landed (later items may be in flight) ...
+        wait_vmem_le<(kQStages - 3) * 4>();
+        __syncthreads();  // ... and every wave's; item n-1's stage (read two items ago) is free
+        dma(min(i0 + n + kQStages - 1, ilast), (n + kQStages - 1) % kQStages);
+        if (n + 1 < nitems) read_frag(n + 1, nxt);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const u32x4 w0 = fp8x8_to_bf16x8(cur.w[j][0], cur.w[j][1]);
+            const u32x4 w1 = fp8x8_to_bf16x8(cur.w[j][2], cur.w[j][3]);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                acc[h] = mfma16x16x32(w0, cur.x[h][j][0], acc[h], bf16_t{});
+                acc[h] = mfma16x16x32(w1, cur.x[h][j][1], acc[h], bf16_t{});
+            }
+        }
+        const int item = i0 + n;
+        if (n != nitems - 1 && (item + 1) % kitems != 0) return;  // segment goes on
+        // end of this workgroup's segment of a unit
+        const int unit = item / kitems;
+        f32x4 v[2] = {accs[0][0] + accs[1][0], accs[0][1] + accs[1][1]};
+        if (seg_start == unit * kitems && item == unit * kitems + kitems - 1) {
+            q_store_y(unit, v);  // whole unit: no other contributor
+        } else if (n != nitems - 1) {
+            // Only the first and the last segment of a run can be partial. The
+            // first one's partial is stored now; its arrival is counted after
+            // the last item, once every outstanding store and load has landed
+            // (waiting here would drain the load pipeline).
+            pend_unit = unit;
+            q_publish(unit, v);
+        } else {
+            last_unit = unit;
+            q_publish(unit, v);
+        }
+        seg_start = item + 1;
+#pragma unroll
+        for (int a2 = 0; a2 < 2; ++a2) accs[a2][0] = accs[a2][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    };
+
+    // items 0 and 1 landed and visible; fragments of item 0 in registers
+    wait_vmem_le<(kQStages - 3) * 4>();
+    __syncthreads();
+    QFrag fa, fb;
+    read_frag(0, fa);
+    for (int n = 0; n < nitems; n += 2) {
+        process(n, fa, fb, accs[0]);
+        if (n + 1 < nitems) process(n + 1, fb, fa, accs[1]);
+    }
+    wait_vmem_le<0>();  // every LDS-DMA write and every partial store has landed
+    __syncthreads();
+    if (tid == 0) {
+        // both arrivals in flight together; the last arrival re-arms the counter
+        int o0 = -1, o1 = -1;
+        if (pend_unit >= 0) o0 = __hip_atomic_fetch_add(&cnt[pend_unit], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (last_unit >= 0) o1 = __hip_atomic_fetch_add(&cnt[last_unit], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool l0 = pend_unit >= 0 && o0 == q_nslots(pend_unit) - 1;
+        const bool l1 = last_unit >= 0 && o1 == q_nslots(last_unit) - 1;
+        if (l0) __hip_atomic_store(&cnt[pend_unit], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (l1) __hip_atomic_store(&cnt[last_unit], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = (l0 ? 1 : 0) | (l1 ? 2 : 0);
+    }
+    __syncthreads();
+    if (s_last) q_reduce2((s_last & 1) ? pend_unit : -1, (s_last & 2) ? last_unit : -1);
+}
+
+
 }  // namespace pyc
 
-extern "C" int pyc_hip_w8a16_launch(int M, int N, int K, const void* X, const void* Wq,
-                                    const float* scale, int relu, void* Y, void* stream) {
+namespace {
+
+// Split-K workspace: fp32 partial slots and per-unit arrival counters, one set
+// per device, grown outside stream capture only (hipMalloc is not capturable)
+// and never freed (kernels of earlier launches may still use it).
+struct W8Workspace {
+    float* part = nullptr;
+    size_t part_bytes = 0;
+    int* cnt = nullptr;
+    int cnt_units = 0;
+};
+constexpr int kMaxDevices = 64;
+W8Workspace g_w8ws[kMaxDevices];
+
+struct W8Plan {
+    int G, base, rem, units, max_slots;
+};
+
+// K % 128 == 0 takes the LDS-staged kernel (items of 128 k), otherwise the
+// register-direct one (items of 64 k).
+bool w8_use_lds(int K) { return K % pyc::kQK == 0; }
+
+W8Plan w8_split(int units, int ksteps, int n_wg) {
+    W8Plan p;
+    p.units = units;
+    const long total = (long)units * ksteps;
+    p.G = (int)(total < n_wg ? total : n_wg);
+    p.base = (int)(total / p.G);
+    p.rem = (int)(total % p.G);
+    p.max_slots = 1;
+    for (int u = 0; u < units; ++u) {
+        const int a = pyc::w8_owner(u * ksteps, p.base, p.rem);
+        const int b = pyc::w8_owner(u * ksteps + ksteps - 1, p.base, p.rem);
+        if (b - a + 1 > p.max_slots) p.max_slots = b - a + 1;
+    }
+    return p;
+}
+
+W8Plan w8_plan(int N, int K, int n_wg) {
+    const int units = (N + pyc::kW8Rows - 1) / pyc::kW8Rows;
+    if (!w8_use_lds(K)) return w8_split(units, (K + pyc::kW8K - 1) / pyc::kW8K, n_wg);
+    // the LDS kernel reduces at most 8 partial slots per unit: use fewer
+    // workgroups (longer runs) when K is so deep that more would share a unit
+    W8Plan p = w8_split(units, K / pyc::kQK, n_wg);
+    while (p.max_slots > 8 && p.G > 1) p = w8_split(units, K / pyc::kQK, p.G * 3 / 4);
+    return p;
+}
+
+int cu_count() {
+    static int n = 0;
+    if (n == 0) {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
+            n = cus;
+        else
+            n = 256;
+    }
+    return n;
+}
+
+// Makes sure the current device's workspace fits the split plan of an N x K
+// layer. Returns false when it cannot (allocation failed).
+bool w8_reserve(const W8Plan& p) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
+    W8Workspace& ws = g_w8ws[dev];
+    const size_t need = (size_t)p.units * p.max_slots * pyc::kW8Waves * pyc::kWave * sizeof(pyc::f32x4);
+    if (ws.part_bytes < need) {
+        float* np = nullptr;
+        if (hipMalloc((void**)&np, need) != hipSuccess) return false;
+        ws.part = np;  // the old buffer is left allocated: in-flight launches may still use it
+        ws.part_bytes = need;
+    }
+    if (ws.cnt_units < p.units) {
+        int* nc = nullptr;
+        if (hipMalloc((void**)&nc, (size_t)p.units * sizeof(int)) != hipSuccess) return false;
+        if (hipMemset(nc, 0, (size_t)p.units * sizeof(int)) != hipSuccess) return false;
+        ws.cnt = nc;
+        ws.cnt_units = p.units;
+    }
+    return true;
+}
+
+}  // namespace
+
+// Allocates the split-K workspace for an N x K layer on the current device,
+// outside any stream capture (callers that capture launches call this first).
+extern "C" int pyc_hip_w8a16_reserve(int N, int K) {
+    if (N <= 0 || K <= 0) return -1;
+    return w8_reserve(w8_plan(N, K, cu_count())) ? 0 : -2;
+}
+
+extern "C" int pyc_hip_w8a16_launch(int M, int N, int K, const void* X, const void* Wq, const float* scale,
+                                    int relu, void* Y, void* stream) {
     using namespace pyc;
-    dim3 grid((N + 16 * kW8Tiles - 1) / (16 * kW8Tiles)), block(kW8Waves * kWave);
-    hipLaunchKernelGGL(w8a16_kernel, grid, block, 0, (hipStream_t)stream, (const uint16_t*)X,
-                       (const uint8_t*)Wq, scale, (uint16_t*)Y, M, N, K, relu);
+    hipStream_t s = (hipStream_t)stream;
+    W8Plan p = w8_plan(N, K, cu_count());
+    float* part = nullptr;
+    int* cnt = nullptr;
+    if (p.max_slots > 1) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(s, &cs) != hipSuccess) return -2;
+        const bool capturing = cs != hipStreamCaptureStatusNone;
+        int dev = 0;
+        const bool have = hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kMaxDevices &&
+                          g_w8ws[dev].part_bytes >= (size_t)p.units * p.max_slots * kW8Waves * kWave * sizeof(f32x4) &&
+                          g_w8ws[dev].cnt_units >= p.units;
+        if (have || (!capturing && w8_reserve(p))) {
+            part = g_w8ws[dev].part;
+            cnt = g_w8ws[dev].cnt;
+        } else {
+            // no workspace: whole units per workgroup
+            const int ksteps = (K + (w8_use_lds(K) ? kQK : kW8K) - 1) / (w8_use_lds(K) ? kQK : kW8K);
+            p.G = p.units;
+            p.base = ksteps;
+            p.rem = 0;
+            p.max_slots = 1;
+        }
+    }
+    if (w8_use_lds(K))
+        hipLaunchKernelGGL(w8a16_lds_kernel, dim3(p.G), dim3(kQWaves * kWave), 0, s, (const uint16_t*)X,
+                           (const uint8_t*)Wq, scale, (uint16_t*)Y, M, N, K, relu, p.base, p.rem, part, cnt,
+                           p.max_slots);
+    else
+        hipLaunchKernelGGL(w8a16_kernel, dim3(p.G), dim3(kW8Waves * kWave), 0, s, (const uint16_t*)X,
+                           (const uint8_t*)Wq, scale, (uint16_t*)Y, M, N, K, relu, p.base, p.rem, part, cnt,
+                           p.max_slots);
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }

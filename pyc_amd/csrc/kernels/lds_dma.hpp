@@ -1,0 +1,40 @@
+// lds_dma.hpp — direct global->LDS loads through buffer descriptors, shared
+// by the kernels that stage tiles in LDS without passing through VGPRs.
+#pragma once
+
+#include "common.hpp"
+
+namespace pyc {
+
+// One LDS-DMA load: lane i's 16 bytes at buffer offset voff + soff land at
+// LDS byte address lds_base + 16*i. Written as inline asm so the compiler does
+// not treat every later LDS read as dependent on it (it would insert a full
+// vmcnt(0) wait after each issue and serialise the loads with the MFMAs); the
+// kernels wait for these loads themselves, before the barrier that publishes
+// them. M0 carries the wave-uniform LDS base; nothing else here uses M0.
+// Offsets at or past the descriptor's byte count read zero.
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+__device__ inline void lds_dma_buf_b128(i32x4 rsrc, uint32_t voff, uint32_t soff, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :
+                 : "s"(lds_base), "v"(voff), "s"(rsrc), "s"(soff)
+                 : "memory", "m0");
+}
+
+// Raw buffer descriptor (CDNA layout): 48-bit base, stride 0, byte count,
+// 32-bit data format. Every field is wave-uniform.
+__device__ inline i32x4 make_buf_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)(uintptr_t)base;
+    i32x4 r;
+    r.x = __builtin_amdgcn_readfirstlane((int32_t)(uint32_t)a);
+    r.y = __builtin_amdgcn_readfirstlane((int32_t)((uint32_t)(a >> 32) & 0xFFFFu));
+    r.z = __builtin_amdgcn_readfirstlane((int32_t)bytes);
+    r.w = 0x00020000;
+    return r;
+}
+
+template <int N> __device__ inline void wait_vmem_le() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+}  // namespace pyc
