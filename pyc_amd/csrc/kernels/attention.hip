@@ -40,12 +40,23 @@ __device__ inline f32x16 mfma32x32x16(const u32x4& a, const u32x4& b, const f32x
                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
 }
 
+// Two floats -> packed pair, round to nearest even (one v_cvt_pk_bf16_f32 /
+// v_cvt_pk_f16_f32 each).
+typedef __attribute__((ext_vector_type(2))) float f32x2_t;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2_t;
 __device__ inline uint32_t pack2(float lo, float hi, bf16_t) {
-    return (uint32_t)elem<bf16_t>::from_f32(lo) | ((uint32_t)elem<bf16_t>::from_f32(hi) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
 }
 __device__ inline uint32_t pack2(float lo, float hi, f16_t) {
-    return (uint32_t)elem<f16_t>::from_f32(lo) | ((uint32_t)elem<f16_t>::from_f32(hi) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, f16x2_t));
 }
+
+// Rescaling threshold of the online softmax (base-2 units): the running max
+// is only raised when a block's max exceeds it by more than this, so most
+// blocks skip the O and l rescale; probabilities then stay below 2^8 before
+// normalisation, and the final O / l is exact whichever max was used.
+constexpr float kAttnRescaleLog2 = 8.0f;
 
 constexpr int kAttnBK = 64;   // keys per LDS block
 
@@ -53,7 +64,9 @@ constexpr int kAttnBK = 64;   // keys per LDS block
 // split over 512 threads keeps every wave within 256 VGPRs), 4 for D=64.
 template <int D> struct attn_cfg { static constexpr int waves = D == 128 ? 8 : 4; };
 
-template <typename T, int D>
+// POS: scale > 0, folded into the exp2 argument; otherwise scores are
+// multiplied by the scale first.
+template <typename T, int D, bool POS>
 __global__ void __launch_bounds__(attn_cfg<D>::waves * kWave, 1)
 attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
                 const uint16_t* __restrict__ Vp, uint16_t* __restrict__ O, int BH, int S,
@@ -186,34 +199,51 @@ attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
                         *reinterpret_cast<const u32x4*>(&ks[krow * D + ((ch ^ (krow & 15)) % KCH) * 8]);
                     s = mfma32x32x16(kf, qf[kk], s, T{});
                 }
-                // lane holds keys key0 + 8*(r/4) + 4h + (r%4) of query qi
-                float mloc = -INFINITY;
+                // lane holds keys key0 + 8*(r/4) + 4h + (r%4) of query qi; scores
+                // are scaled inside the exp2 argument when the scale is positive
+                // (the max of the raw scores then gives the max of the scaled ones)
+                const float c = POS ? scale_log2 : 1.f;
+                if (!POS) {
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int key = key0 + 8 * (r >> 2) + 4 * h + (r & 3);
-                    float v = s[r] * scale_log2;
-                    if ((causal && key > qi) || key >= S) v = -INFINITY;
-                    s[r] = v;
-                    mloc = fmaxf(mloc, v);
+                    for (int r = 0; r < 16; ++r) s[r] *= scale_log2;
                 }
-                mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-                const float m_new = fmaxf(m_run, mloc);
-                const float alpha = exp2f(m_run - m_new);  // m_run = -inf only before key block 0
-                m_run = m_new;
+                const bool edge = (causal && key0 + 31 > q0) || key0 + 31 >= S;  // wave-uniform
+                if (edge) {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int key = key0 + 8 * (r >> 2) + 4 * h + (r & 3);
+                        if ((causal && key > qi) || key >= S) s[r] = -INFINITY;
+                    }
+                }
+                float mloc = s[0];
+#pragma unroll
+                for (int r = 1; r < 16; ++r) mloc = fmaxf(mloc, s[r]);
+                mloc = fmaxf(mloc, __shfl_xor(mloc, 32)) * c;
+                // lazy rescale: only when some lane's max grew past the threshold
+                const bool grow = mloc > m_run + kAttnRescaleLog2;
+                if (__any(grow)) {
+                    const float m_new = fmaxf(m_run, mloc);
+                    // 0 while m_run = -inf (nothing accumulated yet)
+                    const float alpha = m_run == -INFINITY ? 0.f : exp2f(m_run - m_new);
+                    m_run = m_new;
+                    l_run *= alpha;
+#pragma unroll
+                    for (int t = 0; t < DT; ++t)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) acc[t][r] *= alpha;
+                }
+                // a lane whose keys so far are all masked has m_run = -inf
+                const float m_use = m_run == -INFINITY ? 0.f : m_run;
                 float lsum = 0.f;
                 u32x4 pf[2];
 #pragma unroll
                 for (int r = 0; r < 16; r += 2) {
-                    const float p0 = exp2f(s[r] - m_new);
-                    const float p1 = exp2f(s[r + 1] - m_new);
+                    const float p0 = exp2f(fmaf(s[r], c, -m_use));
+                    const float p1 = exp2f(fmaf(s[r + 1], c, -m_use));
                     lsum += p0 + p1;
                     pf[r >> 3][(r & 7) >> 1] = pack2(p0, p1, T{});
                 }
-                l_run = l_run * alpha + lsum;
-#pragma unroll
-                for (int t = 0; t < DT; ++t)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) acc[t][r] *= alpha;
+                l_run += lsum;
                 // O^T[d][q] += Vt[d][keys] P^T[keys][q], two k-steps of 16 keys
 #pragma unroll
                 for (int ks16 = 0; ks16 < 2; ++ks16) {
@@ -261,9 +291,14 @@ static hipError_t launch_attn(int B, int H, int S, int causal, const void* q, co
     const int bq = attn_cfg<D>::waves * 32;
     const int nqb = (S + bq - 1) / bq;
     const float scale_log2 = scale * 1.4426950408889634f;
-    hipLaunchKernelGGL((attn_fwd_kernel<T, D>), dim3(BH * nqb), dim3(attn_cfg<D>::waves * kWave), 0, s,
-                       (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, BH, S,
-                       causal, scale_log2);
+    if (scale_log2 > 0.f)
+        hipLaunchKernelGGL((attn_fwd_kernel<T, D, true>), dim3(BH * nqb), dim3(attn_cfg<D>::waves * kWave), 0, s,
+                           (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, BH, S,
+                           causal, scale_log2);
+    else
+        hipLaunchKernelGGL((attn_fwd_kernel<T, D, false>), dim3(BH * nqb), dim3(attn_cfg<D>::waves * kWave), 0, s,
+                           (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, BH, S,
+                           causal, scale_log2);
     return hipGetLastError();
 }
 

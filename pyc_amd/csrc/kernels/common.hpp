@@ -23,13 +23,8 @@ template <typename T> struct elem;
 template <> struct elem<bf16_t> {
     static constexpr int kBytes = 2;
     __device__ static inline float to_f32(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
-    // Round to nearest even; NaN stays a quiet NaN.
-    __device__ static inline uint16_t from_f32(float f) {
-        uint32_t u = __float_as_uint(f);
-        if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40u);
-        u += 0x7fffu + ((u >> 16) & 1u);
-        return (uint16_t)(u >> 16);
-    }
+    // Round to nearest even, NaN stays a quiet NaN (v_cvt_pk_bf16_f32).
+    __device__ static inline uint16_t from_f32(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 };
 template <> struct elem<f16_t> {
     static constexpr int kBytes = 2;

@@ -42,6 +42,40 @@ def test_attention_vs_oracle(gpu, B, H, S, D, causal):
     _check(got, ref)
 
 
+@pytest.mark.parametrize("case", ["large_logits", "growing_keys", "negative_scale", "zero_scale"])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_softmax_paths(gpu, case, D, causal):
+    """Online-softmax paths: logits whose block maxima jump by far more than
+    the lazy-rescale threshold (large_logits, growing_keys: key j scaled by
+    1 + j/32 so every later block raises the max), and scales <= 0 (the
+    scale is then applied before the max instead of inside exp2)."""
+    torch = gpu
+    B, H, S = 1, 2, 300
+    r = np.random.default_rng(len(case) * 10 + D + causal)
+    q = r.standard_normal((B, H, S, D)).astype(np.float32)
+    k = r.standard_normal((B, H, S, D)).astype(np.float32)
+    v = r.standard_normal((B, H, S, D)).astype(np.float32)
+    scale = 1.0 / np.sqrt(D)
+    if case == "large_logits":
+        q *= 4.0
+        k *= 4.0
+    elif case == "growing_keys":
+        k *= (1.0 + np.arange(S, dtype=np.float32) / 32.0)[None, None, :, None]
+    elif case == "negative_scale":
+        scale = -0.3 / np.sqrt(D)
+    else:
+        scale = 0.0
+    q, k, v = (oracle.f32_to_bf16(t) for t in (q, k, v))
+    Q, K, V = (dev_bits16(torch, t) for t in (q, k, v))
+    O = torch.empty_like(Q)
+    pyc_amd.attention("hip_attention_bf16", Q, K, V, O, causal, scale)
+    torch.cuda.synchronize()
+    got = oracle.bf16_to_f32(host_bits16(O))
+    ref = oracle.attention_f32(*(oracle.bf16_to_f32(t) for t in (q, k, v)), causal, scale)
+    _check(got, ref)
+
+
 def test_attention_config3_sampled_heads(gpu):
     """Config 3 at full size ([8,32,2048,128], causal, scale 1/sqrt(128)): two (b,h)
     pairs against the oracle, plus the size-independent invariant O[:,:,0] = V[:,:,0]
