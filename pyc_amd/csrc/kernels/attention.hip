@@ -25,6 +25,7 @@
 //  * Workgroup order is XCD-aware: ids are remapped so that one XCD walks all
 //    query blocks of a few heads at a time, keeping their K/V in its L2.
 #include "common.hpp"
+#include "lds_dma.hpp"
 
 namespace pyc {
 
@@ -52,17 +53,41 @@ __device__ inline uint32_t pack2(float lo, float hi, f16_t) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, f16x2_t));
 }
 
+// exp2 is the bare v_exp_f32 (its arguments here are <= 8, results that
+// underflow flush to 0, which softmax tolerates), not exp2f's range-reduced
+// sequence of five instructions.
 // Rescaling threshold of the online softmax (base-2 units): the running max
 // is only raised when a block's max exceeds it by more than this, so most
 // blocks skip the O and l rescale; probabilities then stay below 2^8 before
 // normalisation, and the final O / l is exact whichever max was used.
 constexpr float kAttnRescaleLog2 = 8.0f;
 
-constexpr int kAttnBK = 64;   // keys per LDS block
+constexpr int kAttnBK = 64;      // keys per LDS block
+constexpr int kAttnStages = 4;   // K/V blocks in the LDS ring
 
-// Waves per workgroup: 8 for D=128 (one workgroup of 8 waves per CU, K/V staging
-// split over 512 threads keeps every wave within 256 VGPRs), 4 for D=64.
+// Waves per workgroup: 8 for D=128 (one workgroup of 8 waves per CU), 4 for D=64.
 template <int D> struct attn_cfg { static constexpr int waves = D == 128 ? 8 : 4; };
+
+// 16-byte-chunk swizzles of the K and V rows in LDS (CH = D/8 chunks per row).
+// K: chunk c of key row r at c ^ (r % CH); the 32 keys one S^T fragment read
+// touches fall into different bank groups. V: chunk c at c ^ (2r % CH), so
+// the 4 rows x 32 bytes one transpose read of a 16-lane group touches are
+// spread over the bank window.
+template <int CH> __device__ inline int k_swz(int row, int c) { return c ^ (row & (CH - 1)); }
+template <int CH> __device__ inline int v_swz(int row, int c) { return c ^ ((2 * row) & (CH - 1)); }
+
+// LDS transpose read (gfx950 ds_read_b64_tr_b16): within each group of 16
+// lanes, lane i receives element (i & 3) of the 8 bytes that lane
+// 4j + (i >> 2) addresses, as its element j. A group whose lane L addresses
+// row (key0 + L/4), columns (d0 + 4*(L%4)) .. +3 of a row-major [key][d] tile
+// therefore gets, in lane i, the four keys key0..key0+3 of column d0 + i: the
+// V^T operand of O^T = V^T P^T, read from untransposed V.
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+__device__ inline u32x2 lds_read_tr16(const uint16_t* p) {
+    const v4i16_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) v4i16_t*)(__attribute__((address_space(3))) uint16_t*)p);
+    return __builtin_bit_cast(u32x2, v);
+}
 
 // POS: scale > 0, folded into the exp2 argument; otherwise scores are
 // multiplied by the scale first.
@@ -74,21 +99,19 @@ attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
     constexpr int kAttnWaves = attn_cfg<D>::waves;
     constexpr int kAttnBQ = kAttnWaves * 32;  // queries per workgroup
     constexpr int NT = kAttnWaves * kWave;
-    constexpr int KCH = D / 8;                      // 16-byte chunks per K row
-    constexpr int K_LOADS = kAttnBK * KCH / NT;     // per thread
-    constexpr int V_UNITS = (kAttnBK / 2) * KCH / NT;  // (key pair, 8 d) units per thread
-    constexpr int DT = D / 32;                      // 32-wide d tiles of O^T
-    constexpr int KK = D / 16;                      // k-steps of 16 over d for S
-    constexpr int VT_ROW = kAttnBK;                 // elements per Vt row
-    static_assert(K_LOADS * NT == kAttnBK * KCH, "K split");
-    static_assert(V_UNITS * NT == (kAttnBK / 2) * KCH, "V split");
+    constexpr int CH = D / 8;                           // 16-byte chunks per K/V row
+    constexpr int ROWS_PER_DMA = kWave / CH;            // rows one wave-load fills
+    constexpr int DMAS = kAttnBK * CH / NT;             // wave-loads per operand per block per wave
+    constexpr int DT = D / 32;                          // 32-wide d tiles of O^T
+    constexpr int KK = D / 16;                          // k-steps of 16 over d for S
+    constexpr int TILE = kAttnBK * D;                   // elements of one K or V block
+    static_assert(DMAS * NT == kAttnBK * CH, "K/V split");
 
-    __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kAttnBK * D];
-    __shared__ __attribute__((aligned(16))) uint16_t Vt[2][D * VT_ROW];
+    __shared__ __attribute__((aligned(1024))) uint16_t smem[kAttnStages * 2 * TILE];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31;
     const int h = lane >> 5;
 
@@ -123,147 +146,163 @@ attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
     const int kend = causal ? q_last + 1 : S;
     const int nkb = (kend + kAttnBK - 1) / kAttnBK;
 
-    u32x4 rk[K_LOADS];
-    u32x4 rv[V_UNITS][2];
-    auto load_kv = [&](int kb) {
-        const int k0 = kb * kAttnBK;
+    // K/V blocks move global -> LDS by buffer_load ... lds; the descriptors
+    // cover this head only, so rows past S read as zeros.
+    const i32x4 krs = make_buf_rsrc(Kp + base, (uint32_t)((size_t)S * D * 2));
+    const i32x4 vrs = make_buf_rsrc(Vp + base, (uint32_t)((size_t)S * D * 2));
+    const uint32_t lds0 = (uint32_t)(uintptr_t)&smem[0];
+    uint32_t kvo[DMAS], vvo[DMAS], klds[DMAS];
 #pragma unroll
-        for (int i = 0; i < K_LOADS; ++i) {
-            const int qd = tid + i * NT;
-            const int row = qd / KCH, ch = qd % KCH;
-            const int key = k0 + row;
-            rk[i] = key < S ? *reinterpret_cast<const u32x4*>(Kp + base + (size_t)key * D + ch * 8)
-                            : u32x4{0, 0, 0, 0};
+    for (int j = 0; j < DMAS; ++j) {
+        const int row = (j * kAttnWaves + wave) * ROWS_PER_DMA + lane / CH;
+        const int p = lane % CH;
+        kvo[j] = (uint32_t)((row * CH + k_swz<CH>(row, p)) * 16);
+        vvo[j] = (uint32_t)((row * CH + v_swz<CH>(row, p)) * 16);
+        klds[j] = __builtin_amdgcn_readfirstlane(lds0 + (uint32_t)((j * kAttnWaves + wave) * ROWS_PER_DMA * D * 2));
+    }
+    // The block offset goes into the per-lane offset (not the scalar one) so
+    // that the descriptor's range check sees the whole offset of rows past S.
+    auto issue = [&](int kb, int stage) {
+        const uint32_t boff = (uint32_t)kb * kAttnBK * D * 2;
+        const uint32_t sb = (uint32_t)stage * 2 * TILE * 2;
+#pragma unroll
+        for (int j = 0; j < DMAS; ++j) {
+            lds_dma_buf_b128(krs, kvo[j] + boff, 0u, klds[j] + sb);
+            lds_dma_buf_b128(vrs, vvo[j] + boff, 0u, klds[j] + sb + TILE * 2);
         }
+    };
+
+    // V^T fragment addresses: lane group g = lane/16 covers d0 = 16*(g&1) of a
+    // 32-wide d tile and keys 4h..4h+3 / 8+4h..8+4h+3 of a 16-key step
+    // (the key order of the P^T fragment this lane holds).
+    const int gl = lane & 15;
+    const int vcol = 16 * ((lane >> 4) & 1) + 4 * (gl & 3);  // first column this lane addresses, in a d tile
+    const int vrow = 4 * h + (gl >> 2);                      // key offset inside a 16-key step (first read)
+
+    // Two wave groups share every SIMD (wave w and w + W/2 run on the same
+    // SIMD). Group 0 does S, softmax and PV of block kb in iteration kb; group
+    // 1 does PV of block kb-1, then S and softmax of block kb, so one group's
+    // softmax (VALU) runs while the other group's MFMAs run. The ring keeps
+    // two blocks in flight: the stage a DMA refills in iteration kb held block
+    // kb-2, whose last reader (group 1's PV) finished in iteration kb-1.
+    const int grp = wave / (kAttnWaves / 2);
+    u32x4 pf[4];            // P^T fragments of the four 16-key steps
+    bool p_live = false;    // group 1: pf holds block kb-1 awaiting its PV
+
+    // Per-lane LDS element offsets of the fragment reads. Rows a lane reads
+    // differ by multiples of 16 within a block, and both swizzles only see
+    // row bits below 16 (K: row & (CH-1); V: 2*row & (CH-1)), so the swizzled
+    // column depends on the lane and the d tile alone; the row parts are
+    // compile-time immediates.
+    int v_off[DT];
 #pragma unroll
-        for (int u = 0; u < V_UNITS; ++u) {
-            const int qd = tid + u * NT;
-            const int kp = qd / KCH, dc = qd % KCH;
+    for (int t = 0; t < DT; ++t) {
+        const int col = t * 32 + vcol;
+        v_off[t] = vrow * D + v_swz<CH>(vrow, col / 8) * 8 + col % 8;
+    }
+    int k_off[KK];
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) k_off[kk] = l32 * D + k_swz<CH>(l32, kk * 2 + h) * 8;
+
+    auto pv = [&](const uint16_t* vs) {
+#pragma unroll
+        for (int ks16 = 0; ks16 < 4; ++ks16) {
+#pragma unroll
+            for (int t = 0; t < DT; ++t) {
+                const u32x2 a0 = lds_read_tr16(vs + v_off[t] + ks16 * 16 * D);
+                const u32x2 a1 = lds_read_tr16(vs + v_off[t] + (ks16 * 16 + 8) * D);
+                const u32x4 vf = u32x4{a0[0], a0[1], a1[0], a1[1]};
+                acc[t] = mfma32x32x16(vf, pf[ks16], acc[t], T{});
+            }
+        }
+    };
+
+#pragma unroll
+    for (int st = 0; st < kAttnStages - 2; ++st) issue(min(st, nkb - 1), st);
+
+    for (int kb = 0; kb <= nkb; ++kb) {
+        // own loads of block kb landed (block kb+1 may still be in flight) ...
+        wait_vmem_le<2 * DMAS>();
+        __syncthreads();  // ... and every wave's
+        issue(min(kb + kAttnStages - 2, nkb - 1), (kb + kAttnStages - 2) % kAttnStages);
+        if (grp == 1 && p_live) {
+            pv(smem + ((kb - 1) % kAttnStages) * 2 * TILE + TILE);
+            p_live = false;
+        }
+        if (kb == nkb) continue;
+        const uint16_t* ks = smem + (kb % kAttnStages) * 2 * TILE;
+        const uint16_t* vs = ks + TILE;
+        const int key0 = kb * kAttnBK;
+        // wave-uniform skip of blocks entirely above this wave's diagonal
+        if (causal && key0 > q0 + 31) continue;
+        // S^T[key][q] for 64 keys (two 32-key halves, independent MFMA chains)
+        f32x16 sc[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sc[e][r] = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
-                const int key = k0 + 2 * kp + e;
-                rv[u][e] = key < S ? *reinterpret_cast<const u32x4*>(Vp + base + (size_t)key * D + dc * 8)
-                                   : u32x4{0, 0, 0, 0};
+                const u32x4 kf = *reinterpret_cast<const u32x4*>(ks + k_off[kk] + e * 32 * D);
+                sc[e] = mfma32x32x16(kf, qf[kk], sc[e], T{});
             }
         }
-    };
-    auto store_kv = [&](int buf) {
+        // lane holds keys key0 + 32e + 8*(r/4) + 4h + (r%4) of query qi; scores
+        // are scaled inside the exp2 argument when the scale is positive
+        // (the max of the raw scores then gives the max of the scaled ones)
+        const float c = POS ? scale_log2 : 1.f;
+        if (!POS) {
 #pragma unroll
-        for (int i = 0; i < K_LOADS; ++i) {
-            const int qd = tid + i * NT;
-            const int row = qd / KCH, ch = qd % KCH;
-            *reinterpret_cast<u32x4*>(&Ks[buf][row * D + ((ch ^ (row & 15)) % KCH) * 8]) = rk[i];
+            for (int e = 0; e < 2; ++e)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sc[e][r] *= scale_log2;
         }
+        const bool edge = (causal && key0 + kAttnBK - 1 > q0) || key0 + kAttnBK > S;  // wave-uniform
+        if (edge) {
 #pragma unroll
-        for (int u = 0; u < V_UNITS; ++u) {
-            const int qd = tid + u * NT;
-            const int kp = qd / KCH, dc = qd % KCH;
-            const int unit = kp >> 1;         // 8-byte unit (4 keys) holding keys 2kp, 2kp+1
-            const int off = (kp & 1) * 2;     // element offset inside the unit
+            for (int e = 0; e < 2; ++e)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int d = dc * 8 + j;
-                const uint32_t lo = (rv[u][0][j >> 1] >> ((j & 1) * 16)) & 0xffffu;
-                const uint32_t hi = (rv[u][1][j >> 1] >> ((j & 1) * 16)) & 0xffffu;
-                *reinterpret_cast<uint32_t*>(&Vt[buf][d * VT_ROW + ((unit ^ ((d >> 1) & 15)) * 4) + off]) =
-                    lo | (hi << 16);
+                for (int r = 0; r < 16; ++r) {
+                    const int key = key0 + 32 * e + 8 * (r >> 2) + 4 * h + (r & 3);
+                    if ((causal && key > qi) || key >= S) sc[e][r] = -INFINITY;
+                }
+        }
+        float mloc = fmaxf(sc[0][0], sc[1][0]);
+#pragma unroll
+        for (int r = 1; r < 16; ++r) mloc = fmaxf(mloc, fmaxf(sc[0][r], sc[1][r]));
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32)) * c;
+        // lazy rescale: only when some lane's max grew past the threshold
+        const bool grow = mloc > m_run + kAttnRescaleLog2;
+        if (__any(grow)) {
+            const float m_new = fmaxf(m_run, mloc);
+            // 0 while m_run = -inf (nothing accumulated yet)
+            const float alpha = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
+            m_run = m_new;
+            l_run *= alpha;
+#pragma unroll
+            for (int t = 0; t < DT; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[t][r] *= alpha;
+        }
+        // a lane whose keys so far are all masked has m_run = -inf
+        const float m_use = m_run == -INFINITY ? 0.f : m_run;
+        float lsum = 0.f;
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {
+                const float p0 = __builtin_amdgcn_exp2f(fmaf(sc[e][r], c, -m_use));
+                const float p1 = __builtin_amdgcn_exp2f(fmaf(sc[e][r + 1], c, -m_use));
+                lsum += p0 + p1;
+                pf[2 * e + (r >> 3)][(r & 7) >> 1] = pack2(p0, p1, T{});
             }
-        }
-    };
-
-    load_kv(0);
-    store_kv(0);
-    __syncthreads();
-
-    for (int kb = 0; kb < nkb; ++kb) {
-        const int buf = kb & 1;
-        const bool more = kb + 1 < nkb;
-        if (more) load_kv(kb + 1);
-        const uint16_t* ks = Ks[buf];
-        const uint16_t* vt = Vt[buf];
-#pragma unroll
-        for (int sb = 0; sb < kAttnBK / 32; ++sb) {
-            const int key0 = kb * kAttnBK + sb * 32;
-            // wave-uniform skip of sub-blocks entirely above the diagonal / past S
-            const bool skip = (causal && key0 > q0 + 31) || key0 >= S;
-            if (!skip) {
-                // S^T[key][q] for 32 keys x 32 queries
-                f32x16 s;
-#pragma unroll
-                for (int r = 0; r < 16; ++r) s[r] = 0.f;
-                const int krow = sb * 32 + l32;
-#pragma unroll
-                for (int kk = 0; kk < KK; ++kk) {
-                    const int ch = kk * 2 + h;
-                    const u32x4 kf =
-                        *reinterpret_cast<const u32x4*>(&ks[krow * D + ((ch ^ (krow & 15)) % KCH) * 8]);
-                    s = mfma32x32x16(kf, qf[kk], s, T{});
-                }
-                // lane holds keys key0 + 8*(r/4) + 4h + (r%4) of query qi; scores
-                // are scaled inside the exp2 argument when the scale is positive
-                // (the max of the raw scores then gives the max of the scaled ones)
-                const float c = POS ? scale_log2 : 1.f;
-                if (!POS) {
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) s[r] *= scale_log2;
-                }
-                const bool edge = (causal && key0 + 31 > q0) || key0 + 31 >= S;  // wave-uniform
-                if (edge) {
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int key = key0 + 8 * (r >> 2) + 4 * h + (r & 3);
-                        if ((causal && key > qi) || key >= S) s[r] = -INFINITY;
-                    }
-                }
-                float mloc = s[0];
-#pragma unroll
-                for (int r = 1; r < 16; ++r) mloc = fmaxf(mloc, s[r]);
-                mloc = fmaxf(mloc, __shfl_xor(mloc, 32)) * c;
-                // lazy rescale: only when some lane's max grew past the threshold
-                const bool grow = mloc > m_run + kAttnRescaleLog2;
-                if (__any(grow)) {
-                    const float m_new = fmaxf(m_run, mloc);
-                    // 0 while m_run = -inf (nothing accumulated yet)
-                    const float alpha = m_run == -INFINITY ? 0.f : exp2f(m_run - m_new);
-                    m_run = m_new;
-                    l_run *= alpha;
-#pragma unroll
-                    for (int t = 0; t < DT; ++t)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) acc[t][r] *= alpha;
-                }
-                // a lane whose keys so far are all masked has m_run = -inf
-                const float m_use = m_run == -INFINITY ? 0.f : m_run;
-                float lsum = 0.f;
-                u32x4 pf[2];
-#pragma unroll
-                for (int r = 0; r < 16; r += 2) {
-                    const float p0 = exp2f(fmaf(s[r], c, -m_use));
-                    const float p1 = exp2f(fmaf(s[r + 1], c, -m_use));
-                    lsum += p0 + p1;
-                    pf[r >> 3][(r & 7) >> 1] = pack2(p0, p1, T{});
-                }
-                l_run += lsum;
-                // O^T[d][q] += Vt[d][keys] P^T[keys][q], two k-steps of 16 keys
-#pragma unroll
-                for (int ks16 = 0; ks16 < 2; ++ks16) {
-                    const int u0 = sb * 8 + ks16 * 4 + h;
-                    const int u1 = u0 + 2;
-#pragma unroll
-                    for (int t = 0; t < DT; ++t) {
-                        const int d = t * 32 + l32;
-                        const int sw = (d >> 1) & 15;
-                        const u32x2 a0 = *reinterpret_cast<const u32x2*>(&vt[d * VT_ROW + ((u0 ^ sw) * 4)]);
-                        const u32x2 a1 = *reinterpret_cast<const u32x2*>(&vt[d * VT_ROW + ((u1 ^ sw) * 4)]);
-                        const u32x4 vf = u32x4{a0[0], a0[1], a1[0], a1[1]};
-                        acc[t] = mfma32x32x16(vf, pf[ks16], acc[t], T{});
-                    }
-                }
-            }
-        }
-        if (more) store_kv(buf ^ 1);
-        __syncthreads();
+        l_run += lsum;
+        if (grp == 0) pv(vs);
+        else p_live = true;
     }
+    wait_vmem_le<0>();  // no LDS-DMA write may still be pending when the waves end
 
     // finalize: the row sum is split over the two lane halves
     const float l_tot = l_run + __shfl_xor(l_run, 32);
@@ -288,17 +327,17 @@ template <typename T, int D>
 static hipError_t launch_attn(int B, int H, int S, int causal, const void* q, const void* k,
                               const void* v, void* o, float scale, hipStream_t s) {
     const int BH = B * H;
-    const int bq = attn_cfg<D>::waves * 32;
-    const int nqb = (S + bq - 1) / bq;
     const float scale_log2 = scale * 1.4426950408889634f;
+    const uint16_t* qq = (const uint16_t*)q;
+    const uint16_t* kk = (const uint16_t*)k;
+    const uint16_t* vv = (const uint16_t*)v;
+    uint16_t* oo = (uint16_t*)o;
+    const int bq = attn_cfg<D>::waves * 32;
+    const dim3 grid(BH * ((S + bq - 1) / bq)), block(attn_cfg<D>::waves * kWave);
     if (scale_log2 > 0.f)
-        hipLaunchKernelGGL((attn_fwd_kernel<T, D, true>), dim3(BH * nqb), dim3(attn_cfg<D>::waves * kWave), 0, s,
-                           (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, BH, S,
-                           causal, scale_log2);
+        hipLaunchKernelGGL((attn_fwd_kernel<T, D, true>), grid, block, 0, s, qq, kk, vv, oo, BH, S, causal, scale_log2);
     else
-        hipLaunchKernelGGL((attn_fwd_kernel<T, D, false>), dim3(BH * nqb), dim3(attn_cfg<D>::waves * kWave), 0, s,
-                           (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, BH, S,
-                           causal, scale_log2);
+        hipLaunchKernelGGL((attn_fwd_kernel<T, D, false>), grid, block, 0, s, qq, kk, vv, oo, BH, S, causal, scale_log2);
     return hipGetLastError();
 }
 
