@@ -38,10 +38,20 @@ static hipError_t launch_conv(int N, int H, int W, int C, int K, int R, int S, i
 
 }  // namespace pyc
 
+extern "C" int pyc_hip_conv2d_persist_launch(int is_bf16, int Nimg, int H, int W, int C, int Kout, int R, int S,
+                                             int ph, int pw, int sh, int sw, const void* x, const void* w,
+                                             const float* bias, int relu, void* y, void* stream);
+
 extern "C" int pyc_hip_conv2d_launch(int is_bf16, int N, int H, int W, int C, int K, int R, int S, int ph,
                                      int pw, int sh, int sw, const void* x, const void* w,
                                      const float* bias, int relu, void* y, void* stream) {
     using namespace pyc;
+    // whole-tile shapes with C % 64 == 0 take the persistent direct-LDS
+    // implicit GEMM (gemm_nt_lds.hip); it answers 1 when the shape is outside
+    // its preconditions
+    const int rc = pyc_hip_conv2d_persist_launch(is_bf16, N, H, W, C, K, R, S, ph, pw, sh, sw, x, w, bias, relu, y,
+                                                 stream);
+    if (rc != 1) return rc;
     hipStream_t s = (hipStream_t)stream;
     const long P = (H + 2 * ph - R) / sh + 1;
     const long Q = (W + 2 * pw - S) / sw + 1;

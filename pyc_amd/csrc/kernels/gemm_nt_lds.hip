@@ -264,11 +264,23 @@ gemm_nt_lds4k64_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
 // Preconditions: M % 256 == 0, N % 256 == 0, K % 64 == 0, beta == 0, C 16-byte
 // aligned, M*K*2 and N*K*2 below 2^32. Every store is then unconditional, which
 // keeps the per-wave count of outstanding vector-memory operations exact.
-template <typename T, int GA, int GB, int EPI>
+// Implicit-GEMM view of an NHWC convolution for the persistent kernel: A row
+// m = output pixel (n, p, q), A column k = (r, s, c) with c fastest (the KRSC
+// filter is the NT B operand). With C % 64 == 0 one 64-deep K stage is 64
+// consecutive channels of one tap, i.e. 128 contiguous bytes of x: the DMA of
+// a row gathers one whole line, and taps that fall into the padding get an
+// offset past the end of x, which the buffer descriptor reads as zeros.
+struct ConvGeomP {
+    int H, W, C, P, Q, S, sh, sw, ph, pw;
+    uint32_t x_bytes;
+};
+
+template <typename T, int GA, int GB, int EPI, bool CONV = false>
 __global__ void __launch_bounds__(256, 1)
 gemm_nt_persist_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                        uint16_t* __restrict__ C, int M, int N, int K, float alpha,
-                       const float* __restrict__ bias, int tiles_m, int tiles_n, int group_m) {
+                       const float* __restrict__ bias, int tiles_m, int tiles_n, int group_m,
+                       ConvGeomP cg = ConvGeomP{}) {
     constexpr int BK = 64, CH = 8, NT = 256;
     constexpr int ROWS_PER_LOAD = kWave / CH;
     constexpr int LOADS = kD_BM * CH / NT;
@@ -305,16 +317,29 @@ gemm_nt_persist_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
 
     const uint32_t as_base = (uint32_t)(uintptr_t)&As[0];
     const uint32_t bs_base = (uint32_t)(uintptr_t)&Bs[0];
-    const i32x4 a_rsrc = make_buf_rsrc(A, (uint32_t)((size_t)M * K * 2));
+    const i32x4 a_rsrc = make_buf_rsrc(A, CONV ? cg.x_bytes : (uint32_t)((size_t)M * K * 2));
     const i32x4 b_rsrc = make_buf_rsrc(B, (uint32_t)((size_t)N * K * 2));
     uint32_t voff[2 * LOADS];
     uint32_t ldso[2 * LOADS];
+    // CONV: per A row, the pixel index of tap (0,0) (voff[j]) and the packed
+    // input coordinates of tap (0,0), ((ih + 32768) << 16) | (iw + 32768) (hw[j]).
+    uint32_t hw[CONV ? LOADS : 1];
     auto set_tile = [&](int m0, int n0) {
 #pragma unroll
         for (int j = 0; j < LOADS; ++j) {
             const int row = (j * 4 + wave) * ROWS_PER_LOAD + lane / CH;
             const int lch = d_swz(row, lane % CH);
-            voff[j] = (uint32_t)(((size_t)(m0 + row) * K + lch * 8) * 2);
+            if constexpr (CONV) {
+                const int m = m0 + row;
+                const int n = m / (cg.P * cg.Q);
+                const int pq = m - n * (cg.P * cg.Q);
+                const int p = pq / cg.Q, q = pq - (pq / cg.Q) * cg.Q;
+                const int ih = p * cg.sh - cg.ph, iw = q * cg.sw - cg.pw;
+                voff[j] = (uint32_t)((n * cg.H + ih) * cg.W + iw);
+                hw[j] = ((uint32_t)(ih + 32768) << 16) | (uint32_t)(iw + 32768);
+            } else {
+                voff[j] = (uint32_t)(((size_t)(m0 + row) * K + lch * 8) * 2);
+            }
             voff[LOADS + j] = (uint32_t)(((size_t)(n0 + row) * K + lch * 8) * 2);
         }
     };
@@ -324,15 +349,45 @@ gemm_nt_persist_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
         ldso[j] = __builtin_amdgcn_readfirstlane(as_base + off);
         ldso[LOADS + j] = __builtin_amdgcn_readfirstlane(bs_base + off);
     }
-    auto dma = [&](int j, int kt, int buf) {
-        lds_dma_buf_b128(j < LOADS ? a_rsrc : b_rsrc, voff[j], (uint32_t)(kt * BK * 2),
-                         ldso[j] + (uint32_t)buf * STAGE_BYTES);
+    // CONV: stage kt = tap (r, s) x 64 channels from c0; the decomposition is
+    // computed once per stage (stage_tap) rather than per load. A lane's
+    // swizzled chunk is the same for every row it loads (rows it loads differ
+    // by multiples of 8, and the swizzle sees row & 7).
+    struct StageTap {
+        int r, s, c0;
+    };
+    auto stage_tap = [&](int kt) {
+        StageTap t{0, 0, 0};
+        if constexpr (CONV) {
+            const int cst = cg.C / BK;
+            const int tap = kt / cst;
+            t.c0 = (kt - tap * cst) * BK;
+            t.r = tap / cg.S;
+            t.s = tap - t.r * cg.S;
+        }
+        return t;
+    };
+    const uint32_t conv_lch = (uint32_t)d_swz(lane / CH, lane % CH) * 8;
+    auto dma = [&](int j, int kt, int buf, const StageTap& tp) {
+        if (CONV && j < LOADS) {
+            const int ih = (int)(hw[j] >> 16) - 32768 + tp.r;
+            const int iw = (int)(hw[j] & 0xFFFFu) - 32768 + tp.s;
+            const bool in = (unsigned)ih < (unsigned)cg.H && (unsigned)iw < (unsigned)cg.W;
+            const uint32_t off =
+                in ? ((voff[j] + (uint32_t)(tp.r * cg.W + tp.s)) * (uint32_t)cg.C + (uint32_t)tp.c0 + conv_lch) * 2u
+                   : 0xFFFFFFF0u;  // past the end of x: reads zeros
+            lds_dma_buf_b128_u(a_rsrc, off, 0u, ldso[j] + (uint32_t)buf * STAGE_BYTES);
+        } else {
+            lds_dma_buf_b128(j < LOADS ? a_rsrc : b_rsrc, voff[j], (uint32_t)(kt * BK * 2),
+                             ldso[j] + (uint32_t)buf * STAGE_BYTES);
+        }
     };
     auto issue_prologue = [&]() {
+        const StageTap t0 = stage_tap(0), t1 = stage_tap(min(1, ktiles - 1));
 #pragma unroll
-        for (int j = 0; j < 2 * LOADS; ++j) dma(j, 0, 0);
+        for (int j = 0; j < 2 * LOADS; ++j) dma(j, 0, 0, t0);
 #pragma unroll
-        for (int j = 0; j < 2 * LOADS; ++j) dma(j, min(1, ktiles - 1), 1);
+        for (int j = 0; j < 2 * LOADS; ++j) dma(j, min(1, ktiles - 1), 1, t1);
     };
 
     const uint16_t* a_rd[2];
@@ -378,6 +433,7 @@ gemm_nt_persist_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
             const uint32_t nxt = (uint32_t)((kt + 1) & 1) * (kD_BM * BK);
             const int dkt = min(kt + 2, ktiles - 1);
             const int dbuf = kt & 1;
+            const StageTap dtap = stage_tap(dkt);
 #pragma unroll
             for (int g = 0; g < 64; ++g) {
                 if (g == GA) {
@@ -402,7 +458,7 @@ gemm_nt_persist_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
                     if ((g & 1) == 0) fa[1][f] = *reinterpret_cast<const u32x4*>(a_rd[1] + cur + f * 16 * BK);
                     else fb[1][f] = *reinterpret_cast<const u32x4*>(b_rd[1] + cur + f * 16 * BK);
                 }
-                if (g >= GA && g < GA + 16) dma(g - GA, dkt, dbuf);
+                if (g >= GA && g < GA + 16) dma(g - GA, dkt, dbuf, dtap);
                 if (g >= GB && g < GB + 16) {
                     const int f = (g - GB) >> 1;
                     if (((g - GB) & 1) == 0)
@@ -538,5 +594,59 @@ extern "C" int pyc_hip_gemm_nt_lds_launch(int is_bf16, int M, int N, int K, cons
             hipLaunchKernelGGL((gemm_nt_lds4k64_kernel<f16_t, 24, 40>), grid, block, 0, s, a, b, c, M, N, K, alpha,
                                beta, bias, epi, tiles_m, tiles_n, 8);
     }
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+// Implicit-GEMM NHWC conv2d on the persistent kernel (KRSC filter): returns 1
+// when the shape is outside its preconditions (C % 64 == 0, N*P*Q and K_out
+// multiples of 256, x and w below 4 GiB, 16-byte aligned y), 0 on launch, -2
+// on a launch error.
+extern "C" int pyc_hip_conv2d_persist_launch(int is_bf16, int Nimg, int H, int W, int C, int Kout, int R, int S,
+                                             int ph, int pw, int sh, int sw, const void* x, const void* w,
+                                             const float* bias, int relu, void* y, void* stream) {
+    using namespace pyc;
+    if (C % 64 != 0 || sh <= 0 || sw <= 0) return 1;
+    const int P = (H + 2 * ph - R) / sh + 1, Q = (W + 2 * pw - S) / sw + 1;
+    if (P <= 0 || Q <= 0) return 1;
+    const long long M = (long long)Nimg * P * Q;
+    const long long Kg = (long long)R * S * C;
+    if (M % kD_BM != 0 || Kout % kD_BN != 0 || M > 0x7FFFFFFF) return 1;
+    const unsigned long long xb = (unsigned long long)Nimg * H * W * C * 2;
+    if (xb >= 0xFFFFFFF0ull || (unsigned long long)Kout * Kg * 2 > 0xFFFFFFFFull) return 1;
+    if (H >= 32768 || W >= 32768 || ((uintptr_t)y & 15) != 0) return 1;
+    if ((unsigned long long)Nimg * H * W >= (1ull << 31) / (unsigned long long)C) return 1;
+    static int n_cu = 0;
+    if (n_cu == 0) {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
+            n_cu = cus;
+        else
+            n_cu = 256;
+    }
+    const int tiles_m = (int)(M / kD_BM), tiles_n = Kout / kD_BN;
+    const int ntiles = tiles_m * tiles_n;
+    const ConvGeomP cg{H, W, C, P, Q, S, sh, sw, ph, pw, (uint32_t)xb};
+    const int epi = ((bias != nullptr) ? 1 : 0) | (relu ? 2 : 0);
+    const dim3 grid(ntiles < n_cu ? ntiles : n_cu), block(4 * kWave);
+    hipStream_t st = (hipStream_t)stream;
+    const uint16_t* a = (const uint16_t*)x;
+    const uint16_t* b = (const uint16_t*)w;
+    uint16_t* c = (uint16_t*)y;
+#define PYC_CONV(TY, E)                                                                                       \
+    hipLaunchKernelGGL((gemm_nt_persist_kernel<TY, 24, 40, E, true>), grid, block, 0, st, a, b, c, (int)M, Kout, \
+                       (int)Kg, 1.0f, bias, tiles_m, tiles_n, 8, cg)
+    if (is_bf16) {
+        if (epi == 0) PYC_CONV(bf16_t, 0);
+        else if (epi == 1) PYC_CONV(bf16_t, 1);
+        else if (epi == 2) PYC_CONV(bf16_t, 2);
+        else PYC_CONV(bf16_t, 3);
+    } else {
+        if (epi == 0) PYC_CONV(f16_t, 0);
+        else if (epi == 1) PYC_CONV(f16_t, 1);
+        else if (epi == 2) PYC_CONV(f16_t, 2);
+        else PYC_CONV(f16_t, 3);
+    }
+#undef PYC_CONV
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }

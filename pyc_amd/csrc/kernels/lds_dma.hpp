@@ -20,6 +20,13 @@ __device__ inline void lds_dma_buf_b128(i32x4 rsrc, uint32_t voff, uint32_t soff
                  : "s"(lds_base), "v"(voff), "s"(rsrc), "s"(soff)
                  : "memory", "m0");
 }
+// Same, for call sites where the compiler cannot prove the scalar operands
+// wave-uniform: readfirstlane states it (they are uniform by contract).
+__device__ inline void lds_dma_buf_b128_u(i32x4 rsrc, uint32_t voff, uint32_t soff, uint32_t lds_base) {
+    const i32x4 r = i32x4{__builtin_amdgcn_readfirstlane(rsrc.x), __builtin_amdgcn_readfirstlane(rsrc.y),
+                          __builtin_amdgcn_readfirstlane(rsrc.z), __builtin_amdgcn_readfirstlane(rsrc.w)};
+    lds_dma_buf_b128(r, voff, __builtin_amdgcn_readfirstlane(soff), __builtin_amdgcn_readfirstlane(lds_base));
+}
 
 // Raw buffer descriptor (CDNA layout): 48-bit base, stride 0, byte count,
 // 32-bit data format. Every field is wave-uniform.
