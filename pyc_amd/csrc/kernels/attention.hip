@@ -76,6 +76,27 @@ template <int D> struct attn_cfg { static constexpr int waves = D == 128 ? 8 : 4
 template <int CH> __device__ inline int k_swz(int row, int c) { return c ^ (row & (CH - 1)); }
 template <int CH> __device__ inline int v_swz(int row, int c) { return c ^ ((2 * row) & (CH - 1)); }
 
+// Softmax helpers. Scores never hold NaN (masked ones are -inf), so the
+// NaN-propagating maximum is exact here; it lowers to v_maximum3_f32 without
+// the quieting v_max that fmaxf needs.
+__device__ inline float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+// x of lane l ^ 32 (ds_bpermute; xaddr = 4 * (lane ^ 32), computed once).
+// v_permlane32_swap would do this without LDS, but this compiler folds the two
+// results of that intrinsic into one in some uses (max(r0, r1) and r0 + r1
+// became r0 and r0 + r0), so it is not used.
+__device__ inline float other_half(float x, int xaddr) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(xaddr, __builtin_bit_cast(int, x)));
+}
+// acc + lo + hi of a packed pair of probabilities (one v_dot2c_f32_{bf16,f16}):
+// the row sum is taken over the rounded values the PV product uses.
+__device__ inline float add_pair(uint32_t pr, float acc, bf16_t) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pr), bf16x2_t{(__bf16)1.f, (__bf16)1.f}, acc,
+                                           false);
+}
+__device__ inline float add_pair(uint32_t pr, float acc, f16_t) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, pr), f16x2_t{(_Float16)1.f, (_Float16)1.f}, acc, false);
+}
+
 // LDS transpose read (gfx950 ds_read_b64_tr_b16): within each group of 16
 // lanes, lane i receives element (i & 3) of the 8 bytes that lane
 // 4j + (i >> 2) addresses, as its element j. A group whose lane L addresses
@@ -114,6 +135,7 @@ attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31;
     const int h = lane >> 5;
+    const int xaddr = (lane ^ 32) * 4;  // ds_bpermute address of the lane 32 apart
 
     // XCD-aware work order: each XCD gets a contiguous range of (head, q-block) work.
     const int nqb = (S + kAttnBQ - 1) / kAttnBQ;
@@ -261,22 +283,30 @@ attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
         }
         const bool edge = (causal && key0 + kAttnBK - 1 > q0) || key0 + kAttnBK > S;  // wave-uniform
         if (edge) {
+            // key = key0 + 4h + off(e, r) with off = 32e + 8(r/4) + r%4 a
+            // compile-time constant: masked iff off > thr
+            const int thr = (causal ? min(qi, S - 1) : S - 1) - key0 - 4 * h;
 #pragma unroll
             for (int e = 0; e < 2; ++e)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const int key = key0 + 32 * e + 8 * (r >> 2) + 4 * h + (r & 3);
-                    if ((causal && key > qi) || key >= S) sc[e][r] = -INFINITY;
+                    float x = 32 * e + 8 * (r >> 2) + (r & 3) > thr ? -INFINITY : sc[e][r];
+                    asm volatile("" : "+v"(x));  // keeps the masking inside this branch
+                    sc[e][r] = x;
                 }
         }
-        float mloc = fmaxf(sc[0][0], sc[1][0]);
+        float m0 = vmax(sc[0][0], sc[0][1]), m1 = vmax(sc[1][0], sc[1][1]);
 #pragma unroll
-        for (int r = 1; r < 16; ++r) mloc = fmaxf(mloc, fmaxf(sc[0][r], sc[1][r]));
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32)) * c;
+        for (int r = 2; r < 16; r += 2) {
+            m0 = vmax(vmax(m0, sc[0][r]), sc[0][r + 1]);
+            m1 = vmax(vmax(m1, sc[1][r]), sc[1][r + 1]);
+        }
+        const float mh = vmax(m0, m1);
+        const float mloc = vmax(mh, other_half(mh, xaddr)) * c;
         // lazy rescale: only when some lane's max grew past the threshold
         const bool grow = mloc > m_run + kAttnRescaleLog2;
         if (__any(grow)) {
-            const float m_new = fmaxf(m_run, mloc);
+            const float m_new = vmax(m_run, mloc);
             // 0 while m_run = -inf (nothing accumulated yet)
             const float alpha = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
             m_run = m_new;
@@ -288,16 +318,18 @@ attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
         }
         // a lane whose keys so far are all masked has m_run = -inf
         const float m_use = m_run == -INFINITY ? 0.f : m_run;
-        float lsum = 0.f;
+        float ls[2] = {0.f, 0.f};
 #pragma unroll
         for (int e = 0; e < 2; ++e)
 #pragma unroll
             for (int r = 0; r < 16; r += 2) {
                 const float p0 = __builtin_amdgcn_exp2f(fmaf(sc[e][r], c, -m_use));
                 const float p1 = __builtin_amdgcn_exp2f(fmaf(sc[e][r + 1], c, -m_use));
-                lsum += p0 + p1;
-                pf[2 * e + (r >> 3)][(r & 7) >> 1] = pack2(p0, p1, T{});
+                const uint32_t pr = pack2(p0, p1, T{});
+                pf[2 * e + (r >> 3)][(r & 7) >> 1] = pr;
+                ls[e] = add_pair(pr, ls[e], T{});
             }
+        const float lsum = ls[0] + ls[1];
         l_run += lsum;
         if (grp == 0) pv(vs);
         else p_live = true;
@@ -305,7 +337,7 @@ attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
     wait_vmem_le<0>();  // no LDS-DMA write may still be pending when the waves end
 
     // finalize: the row sum is split over the two lane halves
-    const float l_tot = l_run + __shfl_xor(l_run, 32);
+    const float l_tot = l_run + other_half(l_run, xaddr);
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     if (qi < S) {
         uint16_t* orow = O + base + (size_t)qi * D;
