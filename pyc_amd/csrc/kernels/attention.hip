@@ -24,6 +24,8 @@
 //    finite before any fully-masked block is seen.
 //  * Workgroup order is XCD-aware: ids are remapped so that one XCD walks all
 //    query blocks of a few heads at a time, keeping their K/V in its L2.
+#include <type_traits>
+
 #include "common.hpp"
 #include "lds_dma.hpp"
 
@@ -62,11 +64,9 @@ __device__ inline uint32_t pack2(float lo, float hi, f16_t) {
 // normalisation, and the final O / l is exact whichever max was used.
 constexpr float kAttnRescaleLog2 = 8.0f;
 
-constexpr int kAttnBK = 64;      // keys per LDS block
-constexpr int kAttnStages = 4;   // K/V blocks in the LDS ring
-
-// Waves per workgroup: 8 for D=128 (one workgroup of 8 waves per CU), 4 for D=64.
-template <int D> struct attn_cfg { static constexpr int waves = D == 128 ? 8 : 4; };
+constexpr int kAttnBK = 64;     // keys per LDS block
+constexpr int kAttnRing = 4;    // K/V blocks in the LDS ring
+constexpr int kAttnWaves = 8;   // two groups of 4; waves w and w + 4 share a SIMD
 
 // 16-byte-chunk swizzles of the K and V rows in LDS (CH = D/8 chunks per row).
 // K: chunk c of key row r at c ^ (r % CH); the 32 keys one S^T fragment read
@@ -112,61 +112,59 @@ __device__ inline u32x2 lds_read_tr16(const uint16_t* p) {
 
 // POS: scale > 0, folded into the exp2 argument; otherwise scores are
 // multiplied by the scale first.
+//
+// Schedule. Each wave runs, per q-block, the phase sequence
+//   M(-1) V(-1) M(0) V(0) ... V(n-2) M(n-1)
+// with M(k) = S(k+1) = K(k+1) Q^T and O^T += V(k)^T P(k)^T (MFMA work) and
+// V(k) = softmax of S(k+1) into P(k+1) (VALU work), and a workgroup barrier
+// after every phase. Group 1 (waves 4..7) passes one extra barrier first, so
+// it runs one phase behind group 0: while a wave of one group is in an M
+// phase, the wave of the other group on the same SIMD is in a V phase, and
+// the MFMA unit and the VALU work at the same time.
+// K/V block j goes into ring slot j % 4. Every wave issues its part of block
+// j at the start of its phase M(j-3) and waits for it at the end of M(j-2);
+// the barriers that follow make it visible before S(j) (group 0's M(j-1)).
+// The slot's previous block, j-4, was last read by group 1's M(j-4), two
+// global phases before the earliest issue of block j.
 template <typename T, int D, bool POS>
-__global__ void __launch_bounds__(attn_cfg<D>::waves * kWave, 1)
+__global__ void __launch_bounds__(kAttnWaves * kWave, 1)
 attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
                 const uint16_t* __restrict__ Vp, uint16_t* __restrict__ O, int BH, int S,
                 int causal, float scale_log2) {
-    constexpr int kAttnWaves = attn_cfg<D>::waves;
-    constexpr int kAttnBQ = kAttnWaves * 32;  // queries per workgroup
+    constexpr int BQ = kAttnWaves * 32;              // queries per q-block
     constexpr int NT = kAttnWaves * kWave;
-    constexpr int CH = D / 8;                           // 16-byte chunks per K/V row
-    constexpr int ROWS_PER_DMA = kWave / CH;            // rows one wave-load fills
-    constexpr int DMAS = kAttnBK * CH / NT;             // wave-loads per operand per block per wave
-    constexpr int DT = D / 32;                          // 32-wide d tiles of O^T
-    constexpr int KK = D / 16;                          // k-steps of 16 over d for S
-    constexpr int TILE = kAttnBK * D;                   // elements of one K or V block
+    constexpr int CH = D / 8;                        // 16-byte chunks per K/V row
+    constexpr int ROWS_PER_DMA = kWave / CH;         // rows one wave-load fills
+    constexpr int DMAS = kAttnBK * CH / NT;          // wave-loads per operand per block per wave
+    constexpr int DT = D / 32;                       // 32-wide d tiles of O^T
+    constexpr int KK = D / 16;                       // k-steps of 16 over d for S
+    constexpr int TILE = kAttnBK * D;                // elements of one K or V block
     static_assert(DMAS * NT == kAttnBK * CH, "K/V split");
+    static_assert(KK % DT == 0 || DT % 1 == 0, "");
 
-    __shared__ __attribute__((aligned(1024))) uint16_t smem[kAttnStages * 2 * TILE];
+    __shared__ __attribute__((aligned(1024))) uint16_t smem[kAttnRing * 2 * TILE];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = wave / (kAttnWaves / 2);
     const int l32 = lane & 31;
     const int h = lane >> 5;
     const int xaddr = (lane ^ 32) * 4;  // ds_bpermute address of the lane 32 apart
 
-    // XCD-aware work order: each XCD gets a contiguous range of (head, q-block) work.
-    const int nqb = (S + kAttnBQ - 1) / kAttnBQ;
-    const int total = nqb * BH;
+    // Work units: with a causal mask, unit u of a head is the pair of
+    // q-blocks nqb-1-u and u (equal total work for every unit); otherwise
+    // one q-block. Unit order is XCD-aware: each XCD gets a contiguous range
+    // of heads, so the units of one head share K/V in that XCD's L2.
+    const int nqb = (S + BQ - 1) / BQ;
+    const bool pair = causal && nqb > 1;
+    const int units = pair ? (nqb + 1) / 2 : nqb;
+    const int total = units * BH;
     int w = blockIdx.x;
     if ((total & 7) == 0) w = (w & 7) * (total >> 3) + (w >> 3);
-    const int bh = w / nqb;
-    const int qb = nqb - 1 - (w % nqb);  // longest causal blocks of a head first
+    const int bh = w / units;
+    const int u = w - bh * units;
     const size_t base = (size_t)bh * S * D;
-    const int q0 = qb * kAttnBQ + wave * 32;  // this wave's first query
-    const int qi = q0 + l32;                  // this lane's query
-
-    // Q fragments (B operand of S^T = K Q^T): lane holds Q[qi][kk*16 + 8h .. +8].
-    u32x4 qf[KK];
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-        qf[kk] = qi < S ? *reinterpret_cast<const u32x4*>(Q + base + (size_t)qi * D + kk * 16 + h * 8)
-                        : u32x4{0, 0, 0, 0};
-    }
-
-    f32x16 acc[DT];
-#pragma unroll
-    for (int t = 0; t < DT; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
-    float m_run = -INFINITY;  // running max (base-2 scaled) of this lane's query
-    float l_run = 0.f;        // running sum over the keys this lane holds
-
-    const int q_last = min(qb * kAttnBQ + kAttnBQ, S) - 1;
-    const int kend = causal ? q_last + 1 : S;
-    const int nkb = (kend + kAttnBK - 1) / kAttnBK;
 
     // K/V blocks move global -> LDS by buffer_load ... lds; the descriptors
     // cover this head only, so rows past S read as zeros.
@@ -182,40 +180,18 @@ attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
         vvo[j] = (uint32_t)((row * CH + v_swz<CH>(row, p)) * 16);
         klds[j] = __builtin_amdgcn_readfirstlane(lds0 + (uint32_t)((j * kAttnWaves + wave) * ROWS_PER_DMA * D * 2));
     }
-    // The block offset goes into the per-lane offset (not the scalar one) so
-    // that the descriptor's range check sees the whole offset of rows past S.
-    auto issue = [&](int kb, int stage) {
-        const uint32_t boff = (uint32_t)kb * kAttnBK * D * 2;
-        const uint32_t sb = (uint32_t)stage * 2 * TILE * 2;
-#pragma unroll
-        for (int j = 0; j < DMAS; ++j) {
-            lds_dma_buf_b128(krs, kvo[j] + boff, 0u, klds[j] + sb);
-            lds_dma_buf_b128(vrs, vvo[j] + boff, 0u, klds[j] + sb + TILE * 2);
-        }
-    };
-
-    // V^T fragment addresses: lane group g = lane/16 covers d0 = 16*(g&1) of a
-    // 32-wide d tile and keys 4h..4h+3 / 8+4h..8+4h+3 of a 16-key step
-    // (the key order of the P^T fragment this lane holds).
-    const int gl = lane & 15;
-    const int vcol = 16 * ((lane >> 4) & 1) + 4 * (gl & 3);  // first column this lane addresses, in a d tile
-    const int vrow = 4 * h + (gl >> 2);                      // key offset inside a 16-key step (first read)
-
-    // Two wave groups share every SIMD (wave w and w + W/2 run on the same
-    // SIMD). Group 0 does S, softmax and PV of block kb in iteration kb; group
-    // 1 does PV of block kb-1, then S and softmax of block kb, so one group's
-    // softmax (VALU) runs while the other group's MFMAs run. The ring keeps
-    // two blocks in flight: the stage a DMA refills in iteration kb held block
-    // kb-2, whose last reader (group 1's PV) finished in iteration kb-1.
-    const int grp = wave / (kAttnWaves / 2);
-    u32x4 pf[4];            // P^T fragments of the four 16-key steps
-    bool p_live = false;    // group 1: pf holds block kb-1 awaiting its PV
 
     // Per-lane LDS element offsets of the fragment reads. Rows a lane reads
     // differ by multiples of 16 within a block, and both swizzles only see
     // row bits below 16 (K: row & (CH-1); V: 2*row & (CH-1)), so the swizzled
     // column depends on the lane and the d tile alone; the row parts are
     // compile-time immediates.
+    // V^T fragments: lane group g = lane/16 covers d0 = 16*(g&1) of a 32-wide
+    // d tile and keys 4h..4h+3 / 8+4h..8+4h+3 of a 16-key step (the key order
+    // of the P^T fragment this lane holds).
+    const int gl = lane & 15;
+    const int vcol = 16 * ((lane >> 4) & 1) + 4 * (gl & 3);
+    const int vrow = 4 * h + (gl >> 2);
     int v_off[DT];
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
@@ -226,130 +202,226 @@ attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) k_off[kk] = l32 * D + k_swz<CH>(l32, kk * 2 + h) * 8;
 
-    auto pv = [&](const uint16_t* vs) {
-#pragma unroll
-        for (int ks16 = 0; ks16 < 4; ++ks16) {
-#pragma unroll
-            for (int t = 0; t < DT; ++t) {
-                const u32x2 a0 = lds_read_tr16(vs + v_off[t] + ks16 * 16 * D);
-                const u32x2 a1 = lds_read_tr16(vs + v_off[t] + (ks16 * 16 + 8) * D);
-                const u32x4 vf = u32x4{a0[0], a0[1], a1[0], a1[1]};
-                acc[t] = mfma32x32x16(vf, pf[ks16], acc[t], T{});
-            }
-        }
-    };
+    const float c = POS ? scale_log2 : 1.f;
 
-#pragma unroll
-    for (int st = 0; st < kAttnStages - 2; ++st) issue(min(st, nkb - 1), st);
-
-    for (int kb = 0; kb <= nkb; ++kb) {
-        // own loads of block kb landed (block kb+1 may still be in flight) ...
-        wait_vmem_le<2 * DMAS>();
-        __syncthreads();  // ... and every wave's
-        issue(min(kb + kAttnStages - 2, nkb - 1), (kb + kAttnStages - 2) % kAttnStages);
-        if (grp == 1 && p_live) {
-            pv(smem + ((kb - 1) % kAttnStages) * 2 * TILE + TILE);
-            p_live = false;
+    for (int part = 0; part < 2; ++part) {
+        int qb = u;
+        if (pair) {
+            qb = part == 0 ? nqb - 1 - u : u;
+            if (part == 1 && qb == nqb - 1 - u) break;
+        } else if (part == 1) {
+            break;
         }
-        if (kb == nkb) continue;
-        const uint16_t* ks = smem + (kb % kAttnStages) * 2 * TILE;
-        const uint16_t* vs = ks + TILE;
-        const int key0 = kb * kAttnBK;
-        // wave-uniform skip of blocks entirely above this wave's diagonal
-        if (causal && key0 > q0 + 31) continue;
-        // S^T[key][q] for 64 keys (two 32-key halves, independent MFMA chains)
-        f32x16 sc[2];
-#pragma unroll
-        for (int e = 0; e < 2; ++e)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) sc[e][r] = 0.f;
+        if (part == 1) __syncthreads();  // every wave is done with the previous q-block's ring
+
+        const int q0 = qb * BQ + wave * 32;  // this wave's first query
+        const int qi = q0 + l32;             // this lane's query
+        const int q_last = min(qb * BQ + BQ, S) - 1;
+        const int kend = causal ? q_last + 1 : S;
+        const int n = (kend + kAttnBK - 1) / kAttnBK;
+        // blocks past this wave's diagonal are fully masked for it
+        const int n_w = causal ? min(n, (q0 + 31) / kAttnBK + 1) : n;
+
+        // Q fragments (B operand of S^T = K Q^T): lane holds Q[qi][kk*16 + 8h .. +8].
+        u32x4 qf[KK];
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) {
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const u32x4 kf = *reinterpret_cast<const u32x4*>(ks + k_off[kk] + e * 32 * D);
-                sc[e] = mfma32x32x16(kf, qf[kk], sc[e], T{});
-            }
+            qf[kk] = qi < S ? *reinterpret_cast<const u32x4*>(Q + base + (size_t)qi * D + kk * 16 + h * 8)
+                            : u32x4{0, 0, 0, 0};
         }
-        // lane holds keys key0 + 32e + 8*(r/4) + 4h + (r%4) of query qi; scores
-        // are scaled inside the exp2 argument when the scale is positive
-        // (the max of the raw scores then gives the max of the scaled ones)
-        const float c = POS ? scale_log2 : 1.f;
-        if (!POS) {
+        f32x16 acc[DT];
 #pragma unroll
-            for (int e = 0; e < 2; ++e)
+        for (int t = 0; t < DT; ++t)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) sc[e][r] *= scale_log2;
-        }
-        const bool edge = (causal && key0 + kAttnBK - 1 > q0) || key0 + kAttnBK > S;  // wave-uniform
-        if (edge) {
-            // key = key0 + 4h + off(e, r) with off = 32e + 8(r/4) + r%4 a
-            // compile-time constant: masked iff off > thr
-            const int thr = (causal ? min(qi, S - 1) : S - 1) - key0 - 4 * h;
-#pragma unroll
-            for (int e = 0; e < 2; ++e)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    float x = 32 * e + 8 * (r >> 2) + (r & 3) > thr ? -INFINITY : sc[e][r];
-                    asm volatile("" : "+v"(x));  // keeps the masking inside this branch
-                    sc[e][r] = x;
-                }
-        }
-        float m0 = vmax(sc[0][0], sc[0][1]), m1 = vmax(sc[1][0], sc[1][1]);
-#pragma unroll
-        for (int r = 2; r < 16; r += 2) {
-            m0 = vmax(vmax(m0, sc[0][r]), sc[0][r + 1]);
-            m1 = vmax(vmax(m1, sc[1][r]), sc[1][r + 1]);
-        }
-        const float mh = vmax(m0, m1);
-        const float mloc = vmax(mh, other_half(mh, xaddr)) * c;
-        // lazy rescale: only when some lane's max grew past the threshold
-        const bool grow = mloc > m_run + kAttnRescaleLog2;
-        if (__any(grow)) {
-            const float m_new = vmax(m_run, mloc);
-            // 0 while m_run = -inf (nothing accumulated yet)
-            const float alpha = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
-            m_run = m_new;
-            l_run *= alpha;
-#pragma unroll
-            for (int t = 0; t < DT; ++t)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[t][r] *= alpha;
-        }
-        // a lane whose keys so far are all masked has m_run = -inf
-        const float m_use = m_run == -INFINITY ? 0.f : m_run;
-        float ls[2] = {0.f, 0.f};
-#pragma unroll
-        for (int e = 0; e < 2; ++e)
-#pragma unroll
-            for (int r = 0; r < 16; r += 2) {
-                const float p0 = __builtin_amdgcn_exp2f(fmaf(sc[e][r], c, -m_use));
-                const float p1 = __builtin_amdgcn_exp2f(fmaf(sc[e][r + 1], c, -m_use));
-                const uint32_t pr = pack2(p0, p1, T{});
-                pf[2 * e + (r >> 3)][(r & 7) >> 1] = pr;
-                ls[e] = add_pair(pr, ls[e], T{});
-            }
-        const float lsum = ls[0] + ls[1];
-        l_run += lsum;
-        if (grp == 0) pv(vs);
-        else p_live = true;
-    }
-    wait_vmem_le<0>();  // no LDS-DMA write may still be pending when the waves end
+            for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
+        float m_run = -INFINITY;  // running max (base-2 scaled) of this lane's query
+        float l_run = 0.f;        // running sum over the keys this lane holds
+        f32x16 sc[2];             // S^T of the block the next V phase works on
+        u32x4 pf[4];              // P^T fragments of the four 16-key steps of the block the next PV uses
 
-    // finalize: the row sum is split over the two lane halves
-    const float l_tot = l_run + other_half(l_run, xaddr);
-    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    if (qi < S) {
-        uint16_t* orow = O + base + (size_t)qi * D;
+        // The block offset goes into the per-lane offset (not the scalar one)
+        // so that the descriptor's range check sees the whole offset of rows
+        // past S. Blocks past the last are clamped to it (a harmless reload
+        // into a free slot) so that every phase issues the same loads.
+        auto issue = [&](int j) {
+            const uint32_t boff = (uint32_t)min(j, n - 1) * kAttnBK * D * 2;
+            const uint32_t sb = (uint32_t)(j % kAttnRing) * 2 * TILE * 2;
 #pragma unroll
-        for (int t = 0; t < DT; ++t) {
+            for (int jj = 0; jj < DMAS; ++jj) {
+                lds_dma_buf_b128(krs, kvo[jj] + boff, 0u, klds[jj] + sb);
+                lds_dma_buf_b128(vrs, vvo[jj] + boff, 0u, klds[jj] + sb + TILE * 2);
+            }
+        };
+
+        // M phase: S of block js (if DS) and PV of block jp (if DP), interleaved;
+        // the flags are compile-time so that the body is straight-line code.
+        // Step st does the two S MFMAs of k-step st and NPV of the 4*DT PV
+        // MFMAs; the fragments of step st+1 are read from LDS while the MFMAs
+        // of step st run.
+        constexpr int NPV = (4 * DT) / KK;
+        static_assert(NPV * KK == 4 * DT, "PV steps per S step");
+        auto m_phase = [&](auto ds_tag, auto dp_tag, int js, int jp) {
+            constexpr bool DS = decltype(ds_tag)::value, DP = decltype(dp_tag)::value;
+            // slot offsets made opaque so that the per-slot fragment
+            // addresses are formed here (one add each) instead of being
+            // hoisted out of the loop for all four slots (which costs VGPRs)
+            uint32_t so_s = (uint32_t)(js % kAttnRing) * 2 * TILE, so_p = (uint32_t)(jp % kAttnRing) * 2 * TILE + TILE;
+            asm volatile("" : "+s"(so_s), "+s"(so_p));
+            const uint16_t* ks = smem + so_s;
+            const uint16_t* vs = smem + so_p;
+            if constexpr (DS) {
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int d = t * 32 + 8 * g + 4 * h;  // rows 8g + 4h + 0..3 of the d tile
-                u32x2 v;
-                v[0] = pack2(acc[t][4 * g + 0] * inv, acc[t][4 * g + 1] * inv, T{});
-                v[1] = pack2(acc[t][4 * g + 2] * inv, acc[t][4 * g + 3] * inv, T{});
-                *reinterpret_cast<u32x2*>(orow + d) = v;
+                for (int e = 0; e < 2; ++e)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) sc[e][r] = 0.f;
+            }
+            u32x4 kf[2][2], vf[2][NPV];
+            auto load = [&](int st, int b) {
+                if constexpr (DS) {
+#pragma unroll
+                    for (int e = 0; e < 2; ++e)
+                        kf[b][e] = *reinterpret_cast<const u32x4*>(ks + k_off[st] + e * 32 * D);
+                }
+                if constexpr (DP) {
+#pragma unroll
+                    for (int i = 0; i < NPV; ++i) {
+                        const int idx = st * NPV + i;
+                        const int ks16 = idx / DT, t = idx % DT;
+                        const u32x2 a0 = lds_read_tr16(vs + v_off[t] + ks16 * 16 * D);
+                        const u32x2 a1 = lds_read_tr16(vs + v_off[t] + (ks16 * 16 + 8) * D);
+                        vf[b][i] = u32x4{a0[0], a0[1], a1[0], a1[1]};
+                    }
+                }
+            };
+            // per step: first the LDS reads of the next step, then this step's MFMAs
+            constexpr int NRD = (DS ? 2 : 0) + (DP ? 2 * NPV : 0);
+            constexpr int NMF = (DS ? 2 : 0) + (DP ? NPV : 0);
+            load(0, 0);
+#pragma unroll
+            for (int st = 0; st < KK; ++st) {
+                if (st + 1 < KK) {
+                    load(st + 1, (st + 1) & 1);
+                    __builtin_amdgcn_sched_group_barrier(0x100, NRD, 0);  // DS reads
+                }
+                __builtin_amdgcn_sched_group_barrier(0x008, NMF, 0);      // MFMAs
+                if constexpr (DS) {
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) sc[e] = mfma32x32x16(kf[st & 1][e], qf[st], sc[e], T{});
+                }
+                if constexpr (DP) {
+#pragma unroll
+                    for (int i = 0; i < NPV; ++i) {
+                        const int idx = st * NPV + i;
+                        acc[idx % DT] = mfma32x32x16(vf[st & 1][i], pf[idx / DT], acc[idx % DT], T{});
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
+        using yes = std::true_type;
+        using no = std::false_type;
+
+        // V phase: online softmax of block j (scores in sc) into pf.
+        auto v_phase = [&](int j) {
+            const int key0 = j * kAttnBK;
+            if (!POS) {
+#pragma unroll
+                for (int e = 0; e < 2; ++e)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) sc[e][r] *= scale_log2;
+            }
+            // lane holds keys key0 + 32e + 8*(r/4) + 4h + (r%4) of query qi
+            const bool edge = (causal && key0 + kAttnBK - 1 > q0) || key0 + kAttnBK > S;  // wave-uniform
+            if (edge) {
+                // key = key0 + 4h + off(e, r) with off = 32e + 8(r/4) + r%4 a
+                // compile-time constant: masked iff off > thr
+                const int thr = (causal ? min(qi, S - 1) : S - 1) - key0 - 4 * h;
+#pragma unroll
+                for (int e = 0; e < 2; ++e)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        float x = 32 * e + 8 * (r >> 2) + (r & 3) > thr ? -INFINITY : sc[e][r];
+                        asm volatile("" : "+v"(x));  // keeps the masking inside this branch
+                        sc[e][r] = x;
+                    }
+            }
+            float m0 = vmax(sc[0][0], sc[0][1]), m1 = vmax(sc[1][0], sc[1][1]);
+#pragma unroll
+            for (int r = 2; r < 16; r += 2) {
+                m0 = vmax(vmax(m0, sc[0][r]), sc[0][r + 1]);
+                m1 = vmax(vmax(m1, sc[1][r]), sc[1][r + 1]);
+            }
+            const float mh = vmax(m0, m1);
+            const float mloc = vmax(mh, other_half(mh, xaddr)) * c;
+            // lazy rescale: only when some lane's max grew past the threshold
+            const bool grow = mloc > m_run + kAttnRescaleLog2;
+            if (__any(grow)) {
+                const float m_new = vmax(m_run, mloc);
+                // 0 while m_run = -inf (nothing accumulated yet)
+                const float alpha = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
+                m_run = m_new;
+                l_run *= alpha;
+#pragma unroll
+                for (int t = 0; t < DT; ++t)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[t][r] *= alpha;
+            }
+            // a lane whose keys so far are all masked has m_run = -inf
+            const float m_use = m_run == -INFINITY ? 0.f : m_run;
+            float ls[2] = {0.f, 0.f};
+#pragma unroll
+            for (int e = 0; e < 2; ++e)
+#pragma unroll
+                for (int r = 0; r < 16; r += 2) {
+                    const float p0 = __builtin_amdgcn_exp2f(fmaf(sc[e][r], c, -m_use));
+                    const float p1 = __builtin_amdgcn_exp2f(fmaf(sc[e][r + 1], c, -m_use));
+                    const uint32_t pr = pack2(p0, p1, T{});
+                    pf[2 * e + (r >> 3)][(r & 7) >> 1] = pr;
+                    ls[e] = add_pair(pr, ls[e], T{});
+                }
+            l_run += ls[0] + ls[1];
+        };
+
+        issue(0);
+        issue(1);
+        wait_vmem_le<2 * DMAS>();  // own part of block 0 landed ...
+        __syncthreads();           // ... and every wave's
+        if (grp == 1) __syncthreads();  // group 1 runs one phase behind
+        for (int k = -1; k < n; ++k) {
+            // M(k): S(k+1), PV(k)
+            issue(k + 3);
+            // wave-uniform. The last PV of a wave (k = n_w - 1) also computes
+            // an S that is never used: its slot holds finite data (a real
+            // block, or the clamped reload of block n-1), and one variant
+            // fewer keeps the register allocation tight.
+            if (k < 0) m_phase(yes{}, no{}, k + 1, k);
+            else if (k < n_w) m_phase(yes{}, yes{}, k + 1, k);
+            wait_vmem_le<2 * DMAS>();  // own part of block k+2 landed
+            __syncthreads();
+            if (k + 1 < n) {
+                // V(k): softmax of block k+1
+                if (k + 1 < n_w) v_phase(k + 1);
+                __syncthreads();
+            }
+        }
+        if (grp == 0) __syncthreads();
+        wait_vmem_le<0>();  // no LDS-DMA write may still be pending
+
+        // finalize: the row sum is split over the two lane halves
+        const float l_tot = l_run + other_half(l_run, xaddr);
+        const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+        if (qi < S) {
+            uint16_t* orow = O + base + (size_t)qi * D;
+#pragma unroll
+            for (int t = 0; t < DT; ++t) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int d = t * 32 + 8 * g + 4 * h;  // rows 8g + 4h + 0..3 of the d tile
+                    u32x2 v;
+                    v[0] = pack2(acc[t][4 * g + 0] * inv, acc[t][4 * g + 1] * inv, T{});
+                    v[1] = pack2(acc[t][4 * g + 2] * inv, acc[t][4 * g + 3] * inv, T{});
+                    *reinterpret_cast<u32x2*>(orow + d) = v;
+                }
             }
         }
     }
@@ -364,8 +436,10 @@ static hipError_t launch_attn(int B, int H, int S, int causal, const void* q, co
     const uint16_t* kk = (const uint16_t*)k;
     const uint16_t* vv = (const uint16_t*)v;
     uint16_t* oo = (uint16_t*)o;
-    const int bq = attn_cfg<D>::waves * 32;
-    const dim3 grid(BH * ((S + bq - 1) / bq)), block(attn_cfg<D>::waves * kWave);
+    const int bq = kAttnWaves * 32;
+    const int nqb = (S + bq - 1) / bq;
+    const int units = (causal && nqb > 1) ? (nqb + 1) / 2 : nqb;
+    const dim3 grid(BH * units), block(kAttnWaves * kWave);
     if (scale_log2 > 0.f)
         hipLaunchKernelGGL((attn_fwd_kernel<T, D, true>), grid, block, 0, s, qq, kk, vv, oo, BH, S, causal, scale_log2);
     else
