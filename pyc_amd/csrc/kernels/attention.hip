@@ -68,13 +68,22 @@ constexpr int kAttnBK = 64;     // keys per LDS block
 constexpr int kAttnRing = 4;    // K/V blocks in the LDS ring
 constexpr int kAttnWaves = 8;   // two groups of 4; waves w and w + 4 share a SIMD
 
-// 16-byte-chunk swizzles of the K and V rows in LDS (CH = D/8 chunks per row).
-// K: chunk c of key row r at c ^ (r % CH); the 32 keys one S^T fragment read
-// touches fall into different bank groups. V: chunk c at c ^ (2r % CH), so
-// the 4 rows x 32 bytes one transpose read of a 16-lane group touches are
-// spread over the bank window.
-template <int CH> __device__ inline int k_swz(int row, int c) { return c ^ (row & (CH - 1)); }
-template <int CH> __device__ inline int v_swz(int row, int c) { return c ^ ((2 * row) & (CH - 1)); }
+// 16-byte-chunk swizzles of the K and V rows in LDS (CH = D/8 chunks per
+// row; the LDS serves 256 bytes = 64 banks per pass, a D=128 row is 256 bytes
+// and a D=64 row 128). K (ds_read_b128, 16 lanes per pass read one chunk of
+// 16 consecutive rows): chunk c of row r at c ^ (r % 16) for D=128 and at
+// c ^ ((r/2) % 8) for D=64 (row pairs share a bank line). V (ds_read_b64_tr_b16,
+// 32 lanes per pass read chunks 4t..4t+3 of 4 consecutive rows): chunk c at
+// c ^ 4(r % 4) for D=128 and c ^ 4((r/2) % 2) for D=64. Each pass then touches
+// every bank once.
+template <int CH> __device__ inline int k_swz(int row, int c) {
+    if constexpr (CH == 16) return c ^ (row & 15);
+    else return c ^ ((row >> 1) & (CH - 1));
+}
+template <int CH> __device__ inline int v_swz(int row, int c) {
+    if constexpr (CH == 16) return c ^ (4 * (row & 3));
+    else return c ^ (4 * ((row >> 1) & 1));
+}
 
 // Softmax helpers. Scores never hold NaN (masked ones are -inf), so the
 // NaN-propagating maximum is exact here; it lowers to v_maximum3_f32 without
@@ -181,11 +190,11 @@ attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
         klds[j] = __builtin_amdgcn_readfirstlane(lds0 + (uint32_t)((j * kAttnWaves + wave) * ROWS_PER_DMA * D * 2));
     }
 
-    // Per-lane LDS element offsets of the fragment reads. Rows a lane reads
-    // differ by multiples of 16 within a block, and both swizzles only see
-    // row bits below 16 (K: row & (CH-1); V: 2*row & (CH-1)), so the swizzled
-    // column depends on the lane and the d tile alone; the row parts are
-    // compile-time immediates.
+    // Per-lane LDS element offsets of the fragment reads. The K rows a lane
+    // reads differ by multiples of 32 and the V rows by multiples of 8, while
+    // the K swizzle sees only row bits below 16 and the V swizzle only bits
+    // below 4, so the swizzled column depends on the lane and the d tile
+    // alone; the row parts are compile-time immediates.
     // V^T fragments: lane group g = lane/16 covers d0 = 16*(g&1) of a 32-wide
     // d tile and keys 4h..4h+3 / 8+4h..8+4h+3 of a 16-key step (the key order
     // of the P^T fragment this lane holds).
@@ -388,7 +397,12 @@ attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
         __syncthreads();           // ... and every wave's
         if (grp == 1) __syncthreads();  // group 1 runs one phase behind
         for (int k = -1; k < n; ++k) {
-            // M(k): S(k+1), PV(k)
+            // M(k): S(k+1), PV(k). The wave in its M phase gets the higher
+            // issue priority: its MFMAs then go out as soon as the matrix
+            // unit takes them, and the softmax of the SIMD's other wave fills
+            // the remaining issue cycles (left to age order, the older
+            // group's softmax would delay the younger group's MFMAs).
+            __builtin_amdgcn_s_setprio(2);
             issue(k + 3);
             // wave-uniform. The last PV of a wave (k = n_w - 1) also computes
             // an S that is never used: its slot holds finite data (a real
@@ -397,6 +411,7 @@ attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
             if (k < 0) m_phase(yes{}, no{}, k + 1, k);
             else if (k < n_w) m_phase(yes{}, yes{}, k + 1, k);
             wait_vmem_le<2 * DMAS>();  // own part of block k+2 landed
+            __builtin_amdgcn_s_setprio(0);
             __syncthreads();
             if (k + 1 < n) {
                 // V(k): softmax of block k+1
