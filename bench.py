@@ -248,8 +248,9 @@ def wl_decode_chain(torch, args):
         "config": {"workload": "decode_w8a16_chain_8x(32x4096x11008)", "replay": "hipGraph", "launches": 16},
         "roofline": {"bound": "hbm", "achieved": bytes_replay / (ms_kernel * 1e-3) / 1e9, "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": bytes_replay / (ms_kernel * 1e-3) / 1e9 / PEAK_HBM_GBS,
-                     "traffic": None, "kernel_ms": ms_kernel, "algorithmic_bytes_per_replay": bytes_replay,
-                     "weight_bytes": weight_bytes},
+                     "traffic": load_traffic("decode_chain"), "kernel_ms": ms_kernel,
+                     "algorithmic_bytes_per_replay": bytes_replay,
+                     "algorithmic_bytes_per_launch": bytes_replay / (2 * L), "weight_bytes": weight_bytes},
     }
 
 
