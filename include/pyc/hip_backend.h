@@ -73,6 +73,33 @@ int pyc_hip_w8a16_gemm_dispatch(
     const void* X, const void* Wq, const float* scale, int relu,
     void* Y, void* stream);
 
+/* The decode MLP chain in one launch (no reference counterpart; see
+ * pyc_hip_w8a16_gemm_dispatch): for s = 0..nsteps-1,
+ *   X_{s+1} = relu_s?( (X_s * dequant(Wq[s])^T) * scale[s] ),  Y = X_nsteps,
+ * X_0 = X bf16 [M, K[0]], Wq[s] e4m3fn [N[s], K[s]], scale[s] fp32 [N[s]],
+ * Y bf16 [M, N[nsteps-1]]. 1 <= M <= 32, 1 <= nsteps <= 32, K[s] % 128 == 0,
+ * N[s] % 64 == 0, K[s+1] == N[s]. Intermediate activations live in a
+ * library-owned device workspace. Returns -1 on bad arguments, and also when
+ * the stream is being captured and pyc_hip_w8a16_chain_reserve was not called
+ * for this shape first; -2 on a HIP error.
+ * Symbol "hip_w8a16_chain_e4m3". */
+int pyc_hip_w8a16_chain_dispatch(
+    const char* symbol,
+    int M, int nsteps,
+    const void* X, const void* const* Wq, const float* const* scale,
+    const int* N, const int* K, const int* relu,
+    void* Y, void* stream);
+
+/* Allocates the chain workspace for this shape on the current device; call it
+ * outside stream capture before capturing a chain launch. 0, -1 (bad shape),
+ * -2 (HIP error). */
+int pyc_hip_w8a16_chain_reserve(int M, int nsteps, const int* N, const int* K);
+
+/* 1 if a chain launch on the current device gave up waiting for another
+ * workgroup (its output is then invalid), 0 if not, -2 on a HIP error.
+ * Synchronizes the device; clear != 0 resets the flag. */
+int pyc_hip_w8a16_chain_error(int clear);
+
 /* Device properties the bench and the registry report. */
 typedef struct {
     char gcn_arch[64];       /* e.g. "gfx950:sramecc+:xnack-" */

@@ -41,6 +41,12 @@ def _declare(L: C.CDLL) -> None:
     L.pyc_cutlass_conv2d_dispatch.restype = I
     L.pyc_hip_w8a16_gemm_dispatch.argtypes = [S, I, I, I, P, P, P, I, P, P]
     L.pyc_hip_w8a16_gemm_dispatch.restype = I
+    L.pyc_hip_w8a16_chain_dispatch.argtypes = [S, I, I, P, P, P, P, P, P, P, P]
+    L.pyc_hip_w8a16_chain_dispatch.restype = I
+    L.pyc_hip_w8a16_chain_reserve.argtypes = [I, I, P, P]
+    L.pyc_hip_w8a16_chain_reserve.restype = I
+    L.pyc_hip_w8a16_chain_error.argtypes = [I]
+    L.pyc_hip_w8a16_chain_error.restype = I
     L.pyc_hip_device_query.argtypes = [C.POINTER(abi.DeviceInfo)]
     L.pyc_hip_device_query.restype = I
     L.pyc_hip_kernel_symbol_count.argtypes = [S]
@@ -149,6 +155,37 @@ def w8a16_gemm(x, wq, scale, y, relu: bool, stream=None,
     N = wq.shape[0]
     _check(lib().pyc_hip_w8a16_gemm_dispatch(_b(symbol), M, N, K, _ptr(x), _ptr(wq), _ptr(scale),
                                              int(relu), _ptr(y), _stream(stream)), "w8a16 gemm")
+
+
+def _chain_arrays(layers):
+    n = len(layers)
+    wq = (C.c_void_p * n)(*[_ptr(w) for w, _, _ in layers])
+    sc = (C.c_void_p * n)(*[_ptr(s) for _, s, _ in layers])
+    N = (C.c_int * n)(*[int(w.shape[0]) for w, _, _ in layers])
+    K = (C.c_int * n)(*[int(w.shape[1]) for w, _, _ in layers])
+    relu = (C.c_int * n)(*[int(bool(r)) for _, _, r in layers])
+    return n, wq, sc, N, K, relu
+
+
+def w8a16_chain(x, layers, y, stream=None, symbol: str = "hip_w8a16_chain_e4m3") -> None:
+    """The whole chain x -> layers -> y in one launch. layers: [(wq [N,K] uint8
+    e4m3, scale [N] fp32, relu bool), ...], each K equal to the previous N."""
+    n, wq, sc, N, K, relu = _chain_arrays(layers)
+    _check(lib().pyc_hip_w8a16_chain_dispatch(_b(symbol), int(x.shape[0]), n, _ptr(x), C.cast(wq, C.c_void_p),
+                                              C.cast(sc, C.c_void_p), C.cast(N, C.c_void_p), C.cast(K, C.c_void_p),
+                                              C.cast(relu, C.c_void_p), _ptr(y), _stream(stream)), "w8a16 chain")
+
+
+def w8a16_chain_reserve(M: int, layers) -> None:
+    """Allocates the chain workspace (call before capturing a chain launch)."""
+    n, _, _, N, K, _ = _chain_arrays(layers)
+    _check(lib().pyc_hip_w8a16_chain_reserve(M, n, C.cast(N, C.c_void_p), C.cast(K, C.c_void_p)),
+           "w8a16 chain reserve")
+
+
+def w8a16_chain_error(clear: bool = True) -> int:
+    """1 if a chain launch timed out waiting (output invalid), else 0."""
+    return lib().pyc_hip_w8a16_chain_error(int(clear))
 
 
 def device_info() -> abi.DeviceInfo:

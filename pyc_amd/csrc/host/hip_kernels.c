@@ -36,6 +36,9 @@ int pyc_hip_conv2d_launch(int is_bf16, int N, int H, int W, int C, int K, int R,
                           int relu, void* y, void* stream);
 int pyc_hip_w8a16_launch(int M, int N, int K, const void* X, const void* Wq, const float* scale,
                          int relu, void* Y, void* stream);
+int pyc_hip_w8a16_chain_launch(int M, int nsteps, const void* X, const void* const* Wq,
+                               const float* const* scale, const int* N, const int* K, const int* relu,
+                               void* Y, void* stream);
 
 /* ---------------------------------------------------------------- variant table */
 
@@ -225,6 +228,15 @@ int pyc_hip_w8a16_gemm_dispatch(const char* symbol, int M, int N, int K, const v
         return -1;
     }
     return pyc_hip_w8a16_launch(M, N, K, X, Wq, scale, relu ? 1 : 0, Y, stream);
+}
+
+int pyc_hip_w8a16_chain_dispatch(const char* symbol, int M, int nsteps, const void* X, const void* const* Wq,
+                                 const float* const* scale, const int* N, const int* K, const int* relu,
+                                 void* Y, void* stream) {
+    if (!symbol || strcmp(symbol, "hip_w8a16_chain_e4m3") != 0) return -1;
+    if (M <= 0 || M > 32 || nsteps <= 0 || !X || !Wq || !scale || !N || !K || !relu || !Y) return -1;
+    const int rc = pyc_hip_w8a16_chain_launch(M, nsteps, X, Wq, scale, N, K, relu, Y, stream);
+    return rc == -3 ? -1 : rc;
 }
 
 /* ---------------------------------------------------------------- registry */

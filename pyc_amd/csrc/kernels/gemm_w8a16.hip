@@ -41,17 +41,13 @@ constexpr int kW8Rows = 64;  // output channels per unit: 4 MFMA row blocks
 constexpr int kW8K = 64;     // k per item
 
 __device__ inline u32x4 fp8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
-    // Two fp8 per conversion; fp32 -> bf16 by truncation is exact here.
+    // Two fp8 per v_cvt_scalef32_pk_bf16_fp8 (scale 1: exact, e4m3 values have
+    // at most 4 significant bits); bytes 0-1 of a word go to the first pair.
     u32x4 r;
-    const uint32_t w[2] = {lo, hi};
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2;
-        const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8(w[h], false);
-        const f32x2 b = __builtin_amdgcn_cvt_pk_f32_fp8(w[h], true);
-        r[h * 2 + 0] = (__float_as_uint(a[0]) >> 16) | (__float_as_uint(a[1]) & 0xffff0000u);
-        r[h * 2 + 1] = (__float_as_uint(b[0]) >> 16) | (__float_as_uint(b[1]) & 0xffff0000u);
-    }
+    r[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false));
+    r[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true));
+    r[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, false));
+    r[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true));
     return r;
 }
 
@@ -504,6 +500,362 @@ w8a16_lds_kernel(const uint16_t* __restrict__ X, const uint8_t* __restrict__ Wq,
 }
 
 
+
+// ---------------------------------------------------------------------------
+// Whole decode chain in one persistent launch. A chain is a sequence of
+// steps Y_s = relu_s?(scale_s * X_s W_s^T) with X_{s+1} = Y_s, all with M <= 32
+// tokens, K % 128 == 0 and N % 64 == 0. One workgroup per CU walks every step:
+// in each it processes its stream-K share of the step's items with the same
+// LDS pipeline as w8a16_lds_kernel (items of 64 channels x 128 k, split-K
+// partials finished by the last arrival), so no launch boundary, no per-launch
+// pipeline fill and no per-launch tail remain between the steps.
+// Step s+1 may read X_{s+1} only after every unit of step s is finished: each
+// finished unit bumps done[s] (after its Y stores completed) and a workgroup
+// polls done[s] before its first activation load of step s+1. Before that
+// wait it has already issued the weight loads of its first items of step s+1,
+// so the weight stream runs on across the step boundary.
+// Coherence across the XCDs' L2 caches: every intermediate Y_s is a buffer of
+// its own that is written (agent-scope stores, which write through) before
+// anything reads it in the launch, so no L2 holds a stale copy of it; the
+// partial slots and counters use agent-scope accesses as above.
+// The polls are bounded: on a timeout the workgroup sets *err and goes on
+// (the output is then garbage, but the launch ends). The last workgroup to
+// finish re-arms done[] for the next launch (graph replays need no memset).
+// The grid must fit on the device at once (one workgroup per CU).
+constexpr int kChainMaxSteps = 32;
+// Counters (arrival counters, step counters) sit 128 bytes apart: atomics of
+// different units and the polls of the step counters never share a line.
+constexpr int kChainPad = 32;
+struct W8ChainStep {
+    const uint16_t* X;  // [M, K] bf16
+    const uint8_t* W;   // [N, K] e4m3
+    const float* scale; // [N]
+    uint16_t* Y;        // [M, N] bf16
+    float* part;        // split-K slots of this step
+    int* cnt;           // arrival counters of this step's units (kChainPad apart)
+    int N, K, relu, base, rem, max_slots;
+    int gs;             // workgroups with items in this step (the first gs)
+};
+struct W8ChainArgs {
+    W8ChainStep st[kChainMaxSteps];
+    int nsteps, M;
+    int* done;      // finished units per step (kChainPad apart)
+    int* exit_cnt;  // workgroups done with the whole chain
+    int* err;       // nonzero after a wait timed out
+};
+
+__device__ inline void store_coherent_b64(uint16_t* p, uint32_t lo, uint32_t hi) {
+    asm volatile("global_store_dwordx2 %0, %1, off sc1" : : "v"(p), "v"(u32x2{lo, hi}) : "memory");
+}
+
+__global__ void __launch_bounds__(kQWaves * kWave, 1) w8a16_chain_kernel(W8ChainArgs a) {
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[kQStages * kQStageBytes];
+    __shared__ int s_last;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = blockIdx.x;
+    const int G = gridDim.x;
+    const int M = a.M;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)&smem[0];
+
+    // DMA lanes (see w8a16_lds_kernel): instruction q = 2*wave + e moves
+    // weight rows 8q..8q+7 and X tokens 4q..4q+3 of an item.
+    int wrow[2], tok[2];
+    uint32_t wcol[2], xch[2], wlds[2], xlds[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const int q = 2 * wave + e;
+        wrow[e] = 8 * q + lane / 8;
+        wcol[e] = (uint32_t)((((lane % 8) ^ (wrow[e] & 7))) * 16);
+        tok[e] = 4 * q + lane / 16;
+        xch[e] = (uint32_t)(((lane % 16) ^ (tok[e] & 15)) * 16);
+        wlds[e] = __builtin_amdgcn_readfirstlane(lds0 + q * 1024);
+        xlds[e] = __builtin_amdgcn_readfirstlane(lds0 + kQWBytes + q * 1024);
+    }
+    const int lr = lane & 15;
+    const int lg = lane >> 4;
+    const int frow = 16 * wave + lr;
+    uint32_t w_rd[2];
+    uint32_t x_rd[2][2][2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        w_rd[j] = (uint32_t)(frow * kQK + (((lg + 4 * j) ^ (frow & 7)) * 16));
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const int t = 16 * h + lr;
+                x_rd[h][j][q] = (uint32_t)(kQWBytes + t * (kQK * 2) + (((8 * j + 2 * lg + q) ^ (t & 15)) * 16));
+            }
+    }
+    struct QFrag {
+        u32x4 w[2];
+        u32x4 x[2][2][2];
+    };
+    auto read_frag = [&](int n, QFrag& f) {
+        const uint8_t* stage = smem + (n % kQStages) * kQStageBytes;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            f.w[j] = *reinterpret_cast<const u32x4*>(stage + w_rd[j]);
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int q = 0; q < 2; ++q) f.x[h][j][q] = *reinterpret_cast<const u32x4*>(stage + x_rd[h][j][q]);
+        }
+    };
+    // weight / X part of item (unit, kk) of a step, from that step's descriptors
+    auto dma_w = [&](const i32x4& wrs, int K, int unit, int kk, int stage) {
+        const uint32_t sb = (uint32_t)stage * kQStageBytes;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const uint32_t wvo = (uint32_t)(unit * kW8Rows + wrow[e]) * (uint32_t)K + wcol[e];
+            lds_dma_buf_b128_u(wrs, wvo, (uint32_t)(kk * kQK), wlds[e] + sb);
+        }
+    };
+    auto dma_x = [&](const i32x4& xrs, const uint32_t (&xvo)[2], int kk, int stage) {
+        const uint32_t sb = (uint32_t)stage * kQStageBytes;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) lds_dma_buf_b128_u(xrs, xvo[e], (uint32_t)(kk * kQK * 2), xlds[e] + sb);
+    };
+    auto first_item = [&](const W8ChainStep& P) { return g * P.base + min(g, P.rem); };
+    auto num_items = [&](const W8ChainStep& P) { return g < P.gs ? P.base + (g < P.rem ? 1 : 0) : 0; };
+    // bounded wait until *p >= target (one lane polls, the workgroup waits)
+    auto wait_count = [&](int* p, int target) {
+        if (tid == 0) {
+            int it = 0;
+            while (__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+                if (++it > (1 << 20)) {
+                    __hip_atomic_store(a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(16);  // ~1000 cycles: 256 pollers stay off the counter's channel
+            }
+        }
+        __syncthreads();
+    };
+
+    bool w_pre = false;  // weight loads of this step's first items already issued
+    for (int s = 0; s < a.nsteps; ++s) {
+        // this step's descriptor in registers for the whole step
+        const W8ChainStep P = a.st[s];
+        const int N = P.N, K = P.K;
+        const int kitems = K / kQK;
+        const int i0 = first_item(P);
+        const int nitems = num_items(P);
+        const int ilast = i0 + nitems - 1;
+        const i32x4 wrs = make_buf_rsrc(P.W, (uint32_t)((size_t)N * K));
+        const i32x4 xrs = make_buf_rsrc(P.X, (uint32_t)((size_t)M * K * 2));
+        uint32_t xvo[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) xvo[e] = (uint32_t)tok[e] * (uint32_t)K * 2u + xch[e];
+        int fin = 0;  // units of this step finished by this workgroup
+        if (nitems > 0) {
+            // (unit, kk) of item i0 + st, st < kQStages - 1, clamped to the last item
+            const int u0 = i0 / kitems, kk0 = i0 - u0 * kitems;
+            auto pro_item = [&](int st, int& unit, int& kk) {
+                const int t = kk0 + min(st, nitems - 1);
+                unit = u0 + t / kitems;
+                kk = t - (t / kitems) * kitems;
+            };
+            if (!w_pre)
+#pragma unroll
+                for (int st = 0; st < kQStages - 1; ++st) {
+                    int unit, kk;
+                    pro_item(st, unit, kk);
+                    dma_w(wrs, K, unit, kk, st);
+                }
+            // X_s exists once every unit of step s-1 is finished
+            if (s > 0) wait_count(a.done + (s - 1) * kChainPad, a.st[s - 1].N / kW8Rows);
+#pragma unroll
+            for (int st = 0; st < kQStages - 1; ++st) {
+                int unit, kk;
+                pro_item(st, unit, kk);
+                dma_x(xrs, xvo, kk, st);
+            }
+            // next item to load: i0 + kQStages - 1 (clamped), as (unit, kk)
+            int d_unit, d_kk;
+            pro_item(kQStages - 1, d_unit, d_kk);
+            int d_left = nitems - (kQStages - 1);  // loads still to come before the clamp
+
+            auto q_store_y = [&](int unit, const f32x4 (&v)[2]) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int t = 16 * h + lr;
+                    if (t >= M) continue;
+                    const int nch = unit * kW8Rows + 16 * wave + 4 * lg;  // 4 consecutive channels
+                    float y[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        y[r] = v[h][r] * P.scale[nch + r];
+                        if (P.relu) y[r] = y[r] > 0.f ? y[r] : 0.f;
+                    }
+                    store_coherent_b64(P.Y + (size_t)t * N + nch,
+                                       (uint32_t)elem<bf16_t>::from_f32(y[0]) | ((uint32_t)elem<bf16_t>::from_f32(y[1]) << 16),
+                                       (uint32_t)elem<bf16_t>::from_f32(y[2]) | ((uint32_t)elem<bf16_t>::from_f32(y[3]) << 16));
+                }
+            };
+            auto q_slots = [&](int unit) { return P.part + (size_t)unit * P.max_slots * (kQWaves * kWave * 2 * 4); };
+            auto q_first = [&](int unit) { return w8_owner(unit * kitems, P.base, P.rem); };
+            auto q_nslots = [&](int unit) { return w8_owner(unit * kitems + kitems - 1, P.base, P.rem) - q_first(unit) + 1; };
+            auto q_publish = [&](int unit, const f32x4 (&v)[2]) {
+                float* mine = q_slots(unit) + ((size_t)(g - q_first(unit)) * (kQWaves * kWave * 2) + (size_t)tid * 2) * 4;
+                store_coherent_b128(mine, v[0]);
+                store_coherent_b128(mine + 4, v[1]);
+            };
+            auto q_reduce2 = [&](int u0, int u1) {
+                constexpr int kMaxSlots = 8;  // the launcher caps max_slots at this
+                f32x4 got[2][kMaxSlots][2];
+                const int ns[2] = {u0 >= 0 ? q_nslots(u0) : 0, u1 >= 0 ? q_nslots(u1) : 0};
+#pragma unroll
+                for (int uu = 0; uu < 2; ++uu) {
+                    const float* slots = q_slots(uu == 0 ? u0 : u1);
+#pragma unroll
+                    for (int sl = 0; sl < kMaxSlots; ++sl) {
+                        if (sl < ns[uu]) {
+                            const float* src = slots + ((size_t)sl * (kQWaves * kWave * 2) + (size_t)tid * 2) * 4;
+                            got[uu][sl][0] = load_coherent_b128(src);
+                            got[uu][sl][1] = load_coherent_b128(src + 4);
+                        }
+                    }
+                }
+                wait_vmem_le<0>();
+#pragma unroll
+                for (int uu = 0; uu < 2; ++uu) {
+                    if (ns[uu] == 0) continue;
+                    f32x4 sum[2] = {got[uu][0][0], got[uu][0][1]};
+#pragma unroll
+                    for (int sl = 1; sl < kMaxSlots; ++sl)
+                        if (sl < ns[uu]) {
+                            sum[0] += got[uu][sl][0];
+                            sum[1] += got[uu][sl][1];
+                        }
+                    q_store_y(uu == 0 ? u0 : u1, sum);
+                }
+            };
+
+            int seg_start = i0;
+            int pend_unit = -1, last_unit = -1;
+            f32x4 accs[2][2];
+#pragma unroll
+            for (int a2 = 0; a2 < 2; ++a2) accs[a2][0] = accs[a2][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+            auto process = [&](int n, const QFrag& cur, QFrag& nxt, f32x4 (&acc)[2]) {
+                // own loads of items n and n+1 landed. The first items' loads
+                // went out as all weight parts, then all X parts, so fewer
+                // later loads may remain in flight for them.
+                switch (min(n, kQStages - 3)) {
+                    case 0: wait_vmem_le<10>(); break;
+                    case 1: wait_vmem_le<12>(); break;
+                    case 2: wait_vmem_le<14>(); break;
+                    case 3: wait_vmem_le<16>(); break;
+                    case 4: wait_vmem_le<18>(); break;
+                    default: wait_vmem_le<(kQStages - 3) * 4>(); break;
+                }
+                __syncthreads();  // every wave's loads; item n-1's stage is free
+                {
+                    const int stg = (n + kQStages - 1) % kQStages;
+                    dma_w(wrs, K, d_unit, d_kk, stg);
+                    dma_x(xrs, xvo, d_kk, stg);
+                    if (d_left > 1) {  // advance; past the last item keep reloading it
+                        --d_left;
+                        if (++d_kk == kitems) {
+                            d_kk = 0;
+                            ++d_unit;
+                        }
+                    }
+                }
+                if (n + 1 < nitems) read_frag(n + 1, nxt);
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const u32x4 w0 = fp8x8_to_bf16x8(cur.w[j][0], cur.w[j][1]);
+                    const u32x4 w1 = fp8x8_to_bf16x8(cur.w[j][2], cur.w[j][3]);
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        acc[h] = mfma16x16x32(w0, cur.x[h][j][0], acc[h], bf16_t{});
+                        acc[h] = mfma16x16x32(w1, cur.x[h][j][1], acc[h], bf16_t{});
+                    }
+                }
+                const int item = i0 + n;
+                if (n != nitems - 1 && (item + 1) % kitems != 0) return;  // segment goes on
+                const int unit = item / kitems;
+                f32x4 v[2] = {accs[0][0] + accs[1][0], accs[0][1] + accs[1][1]};
+                if (seg_start == unit * kitems && item == unit * kitems + kitems - 1) {
+                    q_store_y(unit, v);  // whole unit: no other contributor
+                    ++fin;
+                } else if (n != nitems - 1) {
+                    pend_unit = unit;  // arrival counted after the last item
+                    q_publish(unit, v);
+                } else {
+                    last_unit = unit;
+                    q_publish(unit, v);
+                }
+                seg_start = item + 1;
+#pragma unroll
+                for (int a2 = 0; a2 < 2; ++a2) accs[a2][0] = accs[a2][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+            };
+
+            wait_vmem_le<10>();  // items 0 and 1 landed (see process) ...
+            __syncthreads();     // ... for every wave
+            QFrag fa, fb;
+            read_frag(0, fa);
+            for (int n = 0; n < nitems; n += 2) {
+                process(n, fa, fb, accs[0]);
+                if (n + 1 < nitems) process(n + 1, fb, fa, accs[1]);
+            }
+            wait_vmem_le<0>();  // every LDS-DMA write, partial and Y store has landed
+            __syncthreads();
+            if (tid == 0) {
+                int o0 = -1, o1 = -1;
+                if (pend_unit >= 0) o0 = __hip_atomic_fetch_add(&P.cnt[pend_unit * kChainPad], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (last_unit >= 0) o1 = __hip_atomic_fetch_add(&P.cnt[last_unit * kChainPad], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const bool l0 = pend_unit >= 0 && o0 == q_nslots(pend_unit) - 1;
+                const bool l1 = last_unit >= 0 && o1 == q_nslots(last_unit) - 1;
+                if (l0) __hip_atomic_store(&P.cnt[pend_unit * kChainPad], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (l1) __hip_atomic_store(&P.cnt[last_unit * kChainPad], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                s_last = (l0 ? 1 : 0) | (l1 ? 2 : 0);
+            }
+            __syncthreads();
+            const int sl = s_last;
+            if (sl) {
+                q_reduce2((sl & 1) ? pend_unit : -1, (sl & 2) ? last_unit : -1);
+                fin += ((sl & 1) ? 1 : 0) + ((sl & 2) ? 1 : 0);
+                wait_vmem_le<0>();  // the Y stores landed
+            }
+            __syncthreads();  // also: every wave is done with the LDS ring
+            if (tid == 0 && fin > 0) __hip_atomic_fetch_add(a.done + s * kChainPad, fin, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        // weight loads of the next step's first items go out before its wait
+        w_pre = false;
+        if (s + 1 < a.nsteps) {
+            const W8ChainStep Q = a.st[s + 1];
+            const int j0 = first_item(Q), nj = num_items(Q);
+            if (nj > 0) {
+                const int qk = Q.K / kQK;
+                const i32x4 qrs = make_buf_rsrc(Q.W, (uint32_t)((size_t)Q.N * Q.K));
+#pragma unroll
+                for (int st = 0; st < kQStages - 1; ++st) {
+                    const int it = j0 + min(st, nj - 1);
+                    const int unit = it / qk;
+                    dma_w(qrs, Q.K, unit, it - unit * qk, st);
+                }
+                w_pre = true;
+            }
+        }
+    }
+    wait_vmem_le<0>();
+    __syncthreads();
+    if (tid == 0) {
+        // the last workgroup out re-arms the step counters: every workgroup
+        // has passed all of its waits by then
+        const int old = __hip_atomic_fetch_add(a.exit_cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old == G - 1) {
+            for (int s = 0; s < a.nsteps; ++s) __hip_atomic_store(a.done + s * kChainPad, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(a.exit_cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
 }  // namespace pyc
 
 namespace {
@@ -635,4 +987,143 @@ extern "C" int pyc_hip_w8a16_launch(int M, int N, int K, const void* X, const vo
                            (const uint8_t*)Wq, scale, (uint16_t*)Y, M, N, K, relu, p.base, p.rem, part, cnt,
                            p.max_slots);
     return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+namespace {
+
+// Chain workspace, one per device, grown outside stream capture only and never
+// freed. A fixed head holds what must start at zero and stay consistent from
+// one launch to the next whatever the chain's shape: the step/exit/error words
+// and the per-step arrival counters (both re-armed by the kernel itself). After
+// it come, laid out per shape, the intermediate activations (one buffer per
+// step) and the split-K slots, which every launch writes before it reads them.
+struct W8ChainWorkspace {
+    uint8_t* buf = nullptr;
+    size_t bytes = 0;
+};
+W8ChainWorkspace g_chainws[kMaxDevices];
+
+constexpr int kChainMaxUnits = 4096;  // N <= 4096 * 64 per step
+// done[] (one 128-byte line per step), then the exit and error words
+constexpr size_t kChainCtlBytes = (size_t)(pyc::kChainMaxSteps + 2) * pyc::kChainPad * sizeof(int);
+constexpr size_t kChainHeadBytes = kChainCtlBytes + (size_t)pyc::kChainMaxSteps * kChainMaxUnits * pyc::kChainPad * sizeof(int);
+
+struct ChainLayout {
+    size_t act[pyc::kChainMaxSteps], part[pyc::kChainMaxSteps];
+    size_t total;
+    W8Plan plan[pyc::kChainMaxSteps];
+};
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// -1: shape outside the chain kernel's preconditions.
+int chain_layout(int M, int nsteps, const int* N, const int* K, ChainLayout& L) {
+    if (M <= 0 || M > 32 || nsteps <= 0 || nsteps > pyc::kChainMaxSteps) return -1;
+    size_t off = kChainHeadBytes;
+    for (int s = 0; s < nsteps; ++s) {
+        if (N[s] <= 0 || K[s] <= 0 || N[s] % pyc::kW8Rows != 0 || K[s] % pyc::kQK != 0) return -1;
+        if (N[s] / pyc::kW8Rows > kChainMaxUnits) return -1;
+        if (s > 0 && K[s] != N[s - 1]) return -1;
+        if ((size_t)N[s] * K[s] >= 0xFFFFFFFFull || (size_t)M * K[s] * 2 >= 0xFFFFFFFFull) return -1;
+        L.plan[s] = w8_plan(N[s], K[s], cu_count());
+        if (L.plan[s].max_slots > 8) return -1;
+        L.act[s] = off;
+        if (s + 1 < nsteps) off += align256((size_t)M * N[s] * 2);
+    }
+    for (int s = 0; s < nsteps; ++s) {
+        L.part[s] = off;
+        off += align256((size_t)L.plan[s].units * L.plan[s].max_slots * pyc::kQWaves * pyc::kWave * 2 * sizeof(pyc::f32x4));
+    }
+    L.total = off;
+    return 0;
+}
+
+// Grows the current device's chain workspace to `bytes` (zeroed).
+bool chain_reserve(size_t bytes) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
+    W8ChainWorkspace& ws = g_chainws[dev];
+    if (ws.bytes >= bytes) return true;
+    uint8_t* nb = nullptr;
+    if (hipMalloc((void**)&nb, bytes) != hipSuccess) return false;
+    if (hipMemset(nb, 0, bytes) != hipSuccess) return false;
+    if (hipDeviceSynchronize() != hipSuccess) return false;
+    ws.buf = nb;  // the old buffer is left allocated: in-flight launches may still use it
+    ws.bytes = bytes;
+    return true;
+}
+
+}  // namespace
+
+// Allocates the chain workspace for this shape on the current device, outside
+// any stream capture (callers that capture the chain call this first).
+extern "C" int pyc_hip_w8a16_chain_reserve(int M, int nsteps, const int* N, const int* K) {
+    ChainLayout L;
+    if (!N || !K || chain_layout(M, nsteps, N, K, L) != 0) return -1;
+    return chain_reserve(L.total) ? 0 : -2;
+}
+
+extern "C" int pyc_hip_w8a16_chain_launch(int M, int nsteps, const void* X, const void* const* Wq,
+                                          const float* const* scale, const int* N, const int* K, const int* relu,
+                                          void* Y, void* stream) {
+    using namespace pyc;
+    ChainLayout L;
+    if (!N || !K || !Wq || !scale || !relu || !X || !Y || chain_layout(M, nsteps, N, K, L) != 0) return -1;
+    hipStream_t st = (hipStream_t)stream;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess) return -2;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return -2;
+    if (g_chainws[dev].bytes < L.total) {
+        if (cs != hipStreamCaptureStatusNone) return -3;  // reserve before capturing
+        if (!chain_reserve(L.total)) return -2;
+    }
+    uint8_t* ws = g_chainws[dev].buf;
+    W8ChainArgs a;
+    a.nsteps = nsteps;
+    a.M = M;
+    int* ctl = (int*)ws;
+    a.done = ctl;
+    a.exit_cnt = ctl + kChainMaxSteps * kChainPad;
+    a.err = ctl + (kChainMaxSteps + 1) * kChainPad;
+    for (int s = 0; s < nsteps; ++s) {
+        W8ChainStep& P = a.st[s];
+        if (!Wq[s] || !scale[s]) return -1;
+        P.X = s == 0 ? (const uint16_t*)X : a.st[s - 1].Y;
+        P.W = (const uint8_t*)Wq[s];
+        P.scale = scale[s];
+        P.Y = s + 1 == nsteps ? (uint16_t*)Y : (uint16_t*)(ws + L.act[s]);
+        P.part = (float*)(ws + L.part[s]);
+        P.cnt = (int*)(ws + kChainCtlBytes) + (size_t)s * kChainMaxUnits * kChainPad;
+        P.N = N[s];
+        P.K = K[s];
+        P.relu = relu[s] ? 1 : 0;
+        P.base = L.plan[s].base;
+        P.rem = L.plan[s].rem;
+        P.max_slots = L.plan[s].max_slots;
+        P.gs = L.plan[s].G;
+    }
+    // one workgroup per CU (the LDS ring allows no second one), all resident together
+    hipLaunchKernelGGL(w8a16_chain_kernel, dim3(cu_count()), dim3(kQWaves * kWave), 0, st, a);
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+// Reads (and with clear != 0 resets) the chain's timeout flag of the current
+// device: 1 if a launch's dependency wait ran out, 0 otherwise, -2 on a HIP
+// error. Synchronizes the device.
+extern "C" int pyc_hip_w8a16_chain_error(int clear) {
+    using namespace pyc;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return -2;
+    W8ChainWorkspace& ws = g_chainws[dev];
+    if (!ws.buf) return 0;
+    if (hipDeviceSynchronize() != hipSuccess) return -2;
+    int* err = (int*)ws.buf + (kChainMaxSteps + 1) * kChainPad;
+    int v = 0;
+    if (hipMemcpy(&v, err, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess) return -2;
+    if (clear && v != 0) {
+        const int z = 0;
+        if (hipMemcpy(err, &z, sizeof(int), hipMemcpyHostToDevice) != hipSuccess) return -2;
+    }
+    return v != 0 ? 1 : 0;
 }
