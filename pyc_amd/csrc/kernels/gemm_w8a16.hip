@@ -31,6 +31,8 @@
 // scale/ReLU, writes Y and resets the counter to zero for the next launch (so
 // graph replays need no memset).
 // Without a workspace every workgroup owns whole units instead.
+#include <stdlib.h>
+
 #include "common.hpp"
 #include "lds_dma.hpp"
 
@@ -523,6 +525,7 @@ w8a16_lds_kernel(const uint16_t* __restrict__ X, const uint8_t* __restrict__ Wq,
 // finish re-arms done[] for the next launch (graph replays need no memset).
 // The grid must fit on the device at once (one workgroup per CU).
 constexpr int kChainMaxSteps = 32;
+constexpr int kCWaves = 8;  // waves w and w+4 share a channel block and split each item's k
 // Counters (arrival counters, step counters) sit 128 bytes apart: atomics of
 // different units and the polls of the step counters never share a line.
 constexpr int kChainPad = 32;
@@ -548,76 +551,81 @@ __device__ inline void store_coherent_b64(uint16_t* p, uint32_t lo, uint32_t hi)
     asm volatile("global_store_dwordx2 %0, %1, off sc1" : : "v"(p), "v"(u32x2{lo, hi}) : "memory");
 }
 
-__global__ void __launch_bounds__(kQWaves * kWave, 1) w8a16_chain_kernel(W8ChainArgs a) {
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[kQStages * kQStageBytes];
+// Chain kernel waits for items n and n+1 of a step (see the kernel).
+template <int ST>
+__device__ inline void wait_first_items(int n) {
+    static_assert(ST >= 4 && ST <= 8, "ring depth");
+    switch (min(n, ST - 3)) {
+        case 0: wait_vmem_le<ST - 3>(); break;
+        case 1: wait_vmem_le<(ST - 2 < 2 * (ST - 3) ? ST - 2 : 2 * (ST - 3))>(); break;
+        case 2: wait_vmem_le<(ST - 1 < 2 * (ST - 3) ? ST - 1 : 2 * (ST - 3))>(); break;
+        case 3: wait_vmem_le<(ST < 2 * (ST - 3) ? ST : 2 * (ST - 3))>(); break;
+        case 4: wait_vmem_le<(ST + 1 < 2 * (ST - 3) ? ST + 1 : 2 * (ST - 3))>(); break;
+        default: wait_vmem_le<2 * (ST - 3)>(); break;
+    }
+}
+
+template <int ST>  // LDS ring stages (ST - 1 items in flight)
+__global__ void __launch_bounds__(kCWaves * kWave, 1) w8a16_chain_kernel(W8ChainArgs a) {
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[ST * kQStageBytes];
     __shared__ int s_last;
+    __shared__ f32x4 s_half[4][kWave][2];  // k-half partials of waves 4..7 at a segment end
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wsub = wave & 3;  // channel block 16*wsub .. +15 of the unit
+    const int jh = wave >> 2;   // k half of every item: 64*jh .. +63
+    const int rtid = wsub * kWave + lane;  // thread index in the 256-thread slot layout
     const int g = blockIdx.x;
     const int G = gridDim.x;
     const int M = a.M;
     const uint32_t lds0 = (uint32_t)(uintptr_t)&smem[0];
 
-    // DMA lanes (see w8a16_lds_kernel): instruction q = 2*wave + e moves
-    // weight rows 8q..8q+7 and X tokens 4q..4q+3 of an item.
-    int wrow[2], tok[2];
-    uint32_t wcol[2], xch[2], wlds[2], xlds[2];
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-        const int q = 2 * wave + e;
-        wrow[e] = 8 * q + lane / 8;
-        wcol[e] = (uint32_t)((((lane % 8) ^ (wrow[e] & 7))) * 16);
-        tok[e] = 4 * q + lane / 16;
-        xch[e] = (uint32_t)(((lane % 16) ^ (tok[e] & 15)) * 16);
-        wlds[e] = __builtin_amdgcn_readfirstlane(lds0 + q * 1024);
-        xlds[e] = __builtin_amdgcn_readfirstlane(lds0 + kQWBytes + q * 1024);
+    // DMA lanes (see w8a16_lds_kernel): wave q's instructions move weight rows
+    // 8q..8q+7 and X tokens 4q..4q+3 of an item.
+    int wrow, tok;
+    uint32_t wcol, xch, wlds, xlds;
+    {
+        const int q = wave;
+        wrow = 8 * q + lane / 8;
+        wcol = (uint32_t)((((lane % 8) ^ (wrow & 7))) * 16);
+        tok = 4 * q + lane / 16;
+        xch = (uint32_t)(((lane % 16) ^ (tok & 15)) * 16);
+        wlds = __builtin_amdgcn_readfirstlane(lds0 + q * 1024);
+        xlds = __builtin_amdgcn_readfirstlane(lds0 + kQWBytes + q * 1024);
     }
     const int lr = lane & 15;
     const int lg = lane >> 4;
-    const int frow = 16 * wave + lr;
-    uint32_t w_rd[2];
-    uint32_t x_rd[2][2][2];
+    const int frow = 16 * wsub + lr;
+    const uint32_t w_rd = (uint32_t)(frow * kQK + (((lg + 4 * jh) ^ (frow & 7)) * 16));
+    uint32_t x_rd[2][2];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        w_rd[j] = (uint32_t)(frow * kQK + (((lg + 4 * j) ^ (frow & 7)) * 16));
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int t = 16 * h + lr;
+            x_rd[h][q] = (uint32_t)(kQWBytes + t * (kQK * 2) + (((8 * jh + 2 * lg + q) ^ (t & 15)) * 16));
+        }
+    struct QFrag {
+        u32x4 w;
+        u32x4 x[2][2];
+    };
+    auto read_frag = [&](int n, QFrag& f) {
+        const uint8_t* stage = smem + (n % ST) * kQStageBytes;
+        f.w = *reinterpret_cast<const u32x4*>(stage + w_rd);
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                const int t = 16 * h + lr;
-                x_rd[h][j][q] = (uint32_t)(kQWBytes + t * (kQK * 2) + (((8 * j + 2 * lg + q) ^ (t & 15)) * 16));
-            }
-    }
-    struct QFrag {
-        u32x4 w[2];
-        u32x4 x[2][2][2];
-    };
-    auto read_frag = [&](int n, QFrag& f) {
-        const uint8_t* stage = smem + (n % kQStages) * kQStageBytes;
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            f.w[j] = *reinterpret_cast<const u32x4*>(stage + w_rd[j]);
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-                for (int q = 0; q < 2; ++q) f.x[h][j][q] = *reinterpret_cast<const u32x4*>(stage + x_rd[h][j][q]);
-        }
+            for (int q = 0; q < 2; ++q) f.x[h][q] = *reinterpret_cast<const u32x4*>(stage + x_rd[h][q]);
     };
     // weight / X part of item (unit, kk) of a step, from that step's descriptors
     auto dma_w = [&](const i32x4& wrs, int K, int unit, int kk, int stage) {
-        const uint32_t sb = (uint32_t)stage * kQStageBytes;
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            const uint32_t wvo = (uint32_t)(unit * kW8Rows + wrow[e]) * (uint32_t)K + wcol[e];
-            lds_dma_buf_b128_u(wrs, wvo, (uint32_t)(kk * kQK), wlds[e] + sb);
-        }
+        const uint32_t wvo = (uint32_t)(unit * kW8Rows + wrow) * (uint32_t)K + wcol;
+        lds_dma_buf_b128_u(wrs, wvo, (uint32_t)(kk * kQK), wlds + (uint32_t)stage * kQStageBytes);
     };
-    auto dma_x = [&](const i32x4& xrs, const uint32_t (&xvo)[2], int kk, int stage) {
-        const uint32_t sb = (uint32_t)stage * kQStageBytes;
-#pragma unroll
-        for (int e = 0; e < 2; ++e) lds_dma_buf_b128_u(xrs, xvo[e], (uint32_t)(kk * kQK * 2), xlds[e] + sb);
+    auto dma_x = [&](const i32x4& xrs, uint32_t xvo, int kk, int stage) {
+        lds_dma_buf_b128_u(xrs, xvo, (uint32_t)(kk * kQK * 2), xlds + (uint32_t)stage * kQStageBytes);
     };
     auto first_item = [&](const W8ChainStep& P) { return g * P.base + min(g, P.rem); };
     auto num_items = [&](const W8ChainStep& P) { return g < P.gs ? P.base + (g < P.rem ? 1 : 0) : 0; };
@@ -647,12 +655,10 @@ __global__ void __launch_bounds__(kQWaves * kWave, 1) w8a16_chain_kernel(W8Chain
         const int ilast = i0 + nitems - 1;
         const i32x4 wrs = make_buf_rsrc(P.W, (uint32_t)((size_t)N * K));
         const i32x4 xrs = make_buf_rsrc(P.X, (uint32_t)((size_t)M * K * 2));
-        uint32_t xvo[2];
-#pragma unroll
-        for (int e = 0; e < 2; ++e) xvo[e] = (uint32_t)tok[e] * (uint32_t)K * 2u + xch[e];
+        const uint32_t xvo = (uint32_t)tok * (uint32_t)K * 2u + xch;
         int fin = 0;  // units of this step finished by this workgroup
         if (nitems > 0) {
-            // (unit, kk) of item i0 + st, st < kQStages - 1, clamped to the last item
+            // (unit, kk) of item i0 + st, st < ST - 1, clamped to the last item
             const int u0 = i0 / kitems, kk0 = i0 - u0 * kitems;
             auto pro_item = [&](int st, int& unit, int& kk) {
                 const int t = kk0 + min(st, nitems - 1);
@@ -661,7 +667,7 @@ __global__ void __launch_bounds__(kQWaves * kWave, 1) w8a16_chain_kernel(W8Chain
             };
             if (!w_pre)
 #pragma unroll
-                for (int st = 0; st < kQStages - 1; ++st) {
+                for (int st = 0; st < ST - 1; ++st) {
                     int unit, kk;
                     pro_item(st, unit, kk);
                     dma_w(wrs, K, unit, kk, st);
@@ -669,22 +675,22 @@ __global__ void __launch_bounds__(kQWaves * kWave, 1) w8a16_chain_kernel(W8Chain
             // X_s exists once every unit of step s-1 is finished
             if (s > 0) wait_count(a.done + (s - 1) * kChainPad, a.st[s - 1].N / kW8Rows);
 #pragma unroll
-            for (int st = 0; st < kQStages - 1; ++st) {
+            for (int st = 0; st < ST - 1; ++st) {
                 int unit, kk;
                 pro_item(st, unit, kk);
                 dma_x(xrs, xvo, kk, st);
             }
-            // next item to load: i0 + kQStages - 1 (clamped), as (unit, kk)
+            // next item to load: i0 + ST - 1 (clamped), as (unit, kk)
             int d_unit, d_kk;
-            pro_item(kQStages - 1, d_unit, d_kk);
-            int d_left = nitems - (kQStages - 1);  // loads still to come before the clamp
+            pro_item(ST - 1, d_unit, d_kk);
+            int d_left = nitems - (ST - 1);  // loads still to come before the clamp
 
             auto q_store_y = [&](int unit, const f32x4 (&v)[2]) {
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     const int t = 16 * h + lr;
                     if (t >= M) continue;
-                    const int nch = unit * kW8Rows + 16 * wave + 4 * lg;  // 4 consecutive channels
+                    const int nch = unit * kW8Rows + 16 * wsub + 4 * lg;  // 4 consecutive channels
                     float y[4];
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
@@ -697,10 +703,11 @@ __global__ void __launch_bounds__(kQWaves * kWave, 1) w8a16_chain_kernel(W8Chain
                 }
             };
             auto q_slots = [&](int unit) { return P.part + (size_t)unit * P.max_slots * (kQWaves * kWave * 2 * 4); };
+            // (slots use the 256-thread layout of w8a16_lds_kernel: waves 0..3 own them)
             auto q_first = [&](int unit) { return w8_owner(unit * kitems, P.base, P.rem); };
             auto q_nslots = [&](int unit) { return w8_owner(unit * kitems + kitems - 1, P.base, P.rem) - q_first(unit) + 1; };
             auto q_publish = [&](int unit, const f32x4 (&v)[2]) {
-                float* mine = q_slots(unit) + ((size_t)(g - q_first(unit)) * (kQWaves * kWave * 2) + (size_t)tid * 2) * 4;
+                float* mine = q_slots(unit) + ((size_t)(g - q_first(unit)) * (kQWaves * kWave * 2) + (size_t)rtid * 2) * 4;
                 store_coherent_b128(mine, v[0]);
                 store_coherent_b128(mine + 4, v[1]);
             };
@@ -714,7 +721,7 @@ __global__ void __launch_bounds__(kQWaves * kWave, 1) w8a16_chain_kernel(W8Chain
 #pragma unroll
                     for (int sl = 0; sl < kMaxSlots; ++sl) {
                         if (sl < ns[uu]) {
-                            const float* src = slots + ((size_t)sl * (kQWaves * kWave * 2) + (size_t)tid * 2) * 4;
+                            const float* src = slots + ((size_t)sl * (kQWaves * kWave * 2) + (size_t)rtid * 2) * 4;
                             got[uu][sl][0] = load_coherent_b128(src);
                             got[uu][sl][1] = load_coherent_b128(src + 4);
                         }
@@ -744,17 +751,14 @@ __global__ void __launch_bounds__(kQWaves * kWave, 1) w8a16_chain_kernel(W8Chain
                 // own loads of items n and n+1 landed. The first items' loads
                 // went out as all weight parts, then all X parts, so fewer
                 // later loads may remain in flight for them.
-                switch (min(n, kQStages - 3)) {
-                    case 0: wait_vmem_le<10>(); break;
-                    case 1: wait_vmem_le<12>(); break;
-                    case 2: wait_vmem_le<14>(); break;
-                    case 3: wait_vmem_le<16>(); break;
-                    case 4: wait_vmem_le<18>(); break;
-                    default: wait_vmem_le<(kQStages - 3) * 4>(); break;
-                }
+                // own loads of items n and n+1 landed. The first items' loads
+                // went out as all weight parts, then all X parts (one
+                // instruction each per wave), so fewer later loads may remain
+                // in flight for them: ST - 3 + n, up to 2 (ST - 3).
+                wait_first_items<ST>(n);
                 __syncthreads();  // every wave's loads; item n-1's stage is free
                 {
-                    const int stg = (n + kQStages - 1) % kQStages;
+                    const int stg = (n + ST - 1) % ST;
                     dma_w(wrs, K, d_unit, d_kk, stg);
                     dma_x(xrs, xvo, d_kk, stg);
                     if (d_left > 1) {  // advance; past the last item keep reloading it
@@ -766,20 +770,42 @@ __global__ void __launch_bounds__(kQWaves * kWave, 1) w8a16_chain_kernel(W8Chain
                     }
                 }
                 if (n + 1 < nitems) read_frag(n + 1, nxt);
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const u32x4 w0 = fp8x8_to_bf16x8(cur.w[j][0], cur.w[j][1]);
-                    const u32x4 w1 = fp8x8_to_bf16x8(cur.w[j][2], cur.w[j][3]);
+                {
+                    const u32x4 w0 = fp8x8_to_bf16x8(cur.w[0], cur.w[1]);
+                    const u32x4 w1 = fp8x8_to_bf16x8(cur.w[2], cur.w[3]);
 #pragma unroll
                     for (int h = 0; h < 2; ++h) {
-                        acc[h] = mfma16x16x32(w0, cur.x[h][j][0], acc[h], bf16_t{});
-                        acc[h] = mfma16x16x32(w1, cur.x[h][j][1], acc[h], bf16_t{});
+                        acc[h] = mfma16x16x32(w0, cur.x[h][0], acc[h], bf16_t{});
+                        acc[h] = mfma16x16x32(w1, cur.x[h][1], acc[h], bf16_t{});
                     }
                 }
                 const int item = i0 + n;
                 if (n != nitems - 1 && (item + 1) % kitems != 0) return;  // segment goes on
                 const int unit = item / kitems;
                 f32x4 v[2] = {accs[0][0] + accs[1][0], accs[0][1] + accs[1][1]};
+                // the two k halves of a channel block meet in waves 0..3
+                if (jh == 1) {
+                    s_half[wsub][lane][0] = v[0];
+                    s_half[wsub][lane][1] = v[1];
+                }
+                __syncthreads();
+                if (jh == 0) {
+                    v[0] += s_half[wsub][lane][0];
+                    v[1] += s_half[wsub][lane][1];
+                }
+#pragma unroll
+                for (int a2 = 0; a2 < 2; ++a2) accs[a2][0] = accs[a2][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+                if (jh == 1) {
+                    // waves 4..7 only track the segment state
+                    if (!(seg_start == unit * kitems && item == unit * kitems + kitems - 1)) {
+                        if (n != nitems - 1) pend_unit = unit;
+                        else last_unit = unit;
+                    } else {
+                        ++fin;
+                    }
+                    seg_start = item + 1;
+                    return;
+                }
                 if (seg_start == unit * kitems && item == unit * kitems + kitems - 1) {
                     q_store_y(unit, v);  // whole unit: no other contributor
                     ++fin;
@@ -795,7 +821,7 @@ __global__ void __launch_bounds__(kQWaves * kWave, 1) w8a16_chain_kernel(W8Chain
                 for (int a2 = 0; a2 < 2; ++a2) accs[a2][0] = accs[a2][1] = f32x4{0.f, 0.f, 0.f, 0.f};
             };
 
-            wait_vmem_le<10>();  // items 0 and 1 landed (see process) ...
+            wait_first_items<ST>(0);  // items 0 and 1 landed (see process) ...
             __syncthreads();     // ... for every wave
             QFrag fa, fb;
             read_frag(0, fa);
@@ -818,7 +844,7 @@ __global__ void __launch_bounds__(kQWaves * kWave, 1) w8a16_chain_kernel(W8Chain
             __syncthreads();
             const int sl = s_last;
             if (sl) {
-                q_reduce2((sl & 1) ? pend_unit : -1, (sl & 2) ? last_unit : -1);
+                if (jh == 0) q_reduce2((sl & 1) ? pend_unit : -1, (sl & 2) ? last_unit : -1);
                 fin += ((sl & 1) ? 1 : 0) + ((sl & 2) ? 1 : 0);
                 wait_vmem_le<0>();  // the Y stores landed
             }
@@ -834,7 +860,7 @@ __global__ void __launch_bounds__(kQWaves * kWave, 1) w8a16_chain_kernel(W8Chain
                 const int qk = Q.K / kQK;
                 const i32x4 qrs = make_buf_rsrc(Q.W, (uint32_t)((size_t)Q.N * Q.K));
 #pragma unroll
-                for (int st = 0; st < kQStages - 1; ++st) {
+                for (int st = 0; st < ST - 1; ++st) {
                     const int it = j0 + min(st, nj - 1);
                     const int unit = it / qk;
                     dma_w(qrs, Q.K, unit, it - unit * qk, st);
@@ -1104,7 +1130,19 @@ extern "C" int pyc_hip_w8a16_chain_launch(int M, int nsteps, const void* X, cons
         P.gs = L.plan[s].G;
     }
     // one workgroup per CU (the LDS ring allows no second one), all resident together
-    hipLaunchKernelGGL(w8a16_chain_kernel, dim3(cu_count()), dim3(kQWaves * kWave), 0, st, a);
+    // ring depth: fewer loads in flight shorten the queueing that the step
+    // boundary's round trips wait behind (PYC_CHAIN_STAGES overrides)
+    static int stages = 0;
+    if (stages == 0) {
+        const char* e = getenv("PYC_CHAIN_STAGES");
+        const int v = e ? atoi(e) : 0;
+        stages = (v == 4 || v == 5 || v == 6 || v == 8) ? v : 6;
+    }
+    const dim3 grid(cu_count()), block(kCWaves * kWave);
+    if (stages == 4) hipLaunchKernelGGL(w8a16_chain_kernel<4>, grid, block, 0, st, a);
+    else if (stages == 5) hipLaunchKernelGGL(w8a16_chain_kernel<5>, grid, block, 0, st, a);
+    else if (stages == 6) hipLaunchKernelGGL(w8a16_chain_kernel<6>, grid, block, 0, st, a);
+    else hipLaunchKernelGGL(w8a16_chain_kernel<8>, grid, block, 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 

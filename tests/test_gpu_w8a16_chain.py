@@ -1,12 +1,14 @@
 """GPU parity: the whole fp8-weight decode chain in one launch
 (pyc_hip_w8a16_chain_dispatch).
 
-The chain kernel splits every step's items exactly as the single-layer kernel
-does and sums the split-K partials in the same order, so its output must be
-bit-identical to the same layers run one launch at a time; the single-layer
-kernel is itself checked against the CPU oracle (tests/test_gpu_w8a16.py),
-and small chains are checked against the oracle here too (tolerance as there:
-max|got-ref| <= 2e-2 * max|ref|)."""
+The chain kernel splits every step's items as the single-layer kernel does
+but sums each item's two k halves in different waves, so its fp32 sums are
+ordered differently: it is checked against the same layers run one launch at
+a time (themselves checked against the CPU oracle in tests/test_gpu_w8a16.py)
+and, for chains the oracle finishes quickly, against the oracle directly,
+both to BASELINE's bar max|got-ref| <= 2e-2 * max|ref|. Repeated launches and
+graph replays of one chain must agree bit for bit (the kernel is
+deterministic)."""
 import ctypes as C
 
 import numpy as np
@@ -59,7 +61,8 @@ def test_chain_matches_layers(gpu, M, dims, relus):
     ref_dev = _sequential(torch, X, layers)
     torch.cuda.synchronize()
     assert pyc_amd.w8a16_chain_error() == 0
-    assert torch.equal(Y, ref_dev), "chain differs from the layer-by-layer launches"
+    got = Y.float().cpu().numpy()
+    assert rel_max_err(got, ref_dev.float().cpu().numpy()) <= 2e-2, "chain vs layer-by-layer launches"
     if dims[0] * dims[1] <= 2048 * 3072:
         cur = x
         for (wq, s), r in zip(ws, relus):
@@ -83,7 +86,11 @@ def test_chain_decode_config(gpu):
         ref = _sequential(torch, X, layers)
         torch.cuda.synchronize()
         assert pyc_amd.w8a16_chain_error() == 0
-        assert torch.equal(Y, ref), f"input {seed}: chain differs from the layer-by-layer launches"
+        assert rel_max_err(Y.float().cpu().numpy(), ref.float().cpu().numpy()) <= 2e-2, f"input {seed}"
+        Y2 = torch.empty_like(Y)
+        pyc_amd.w8a16_chain(X, layers, Y2)
+        torch.cuda.synchronize()
+        assert torch.equal(Y, Y2), f"input {seed}: a second launch differs"
 
 
 def test_chain_graph_replay(gpu):
@@ -120,8 +127,8 @@ def test_chain_graph_replay(gpu):
         pyc_amd.w8a16_chain(Xo, other, Yo)
         torch.cuda.synchronize()
         assert torch.equal(Yg, Ye), f"replay {rep} differs from the eager chain"
-    assert torch.equal(Yo, _sequential(torch, Xo, other))
-    assert torch.equal(Ye, _sequential(torch, X, layers))
+    assert rel_max_err(Yo.float().cpu().numpy(), _sequential(torch, Xo, other).float().cpu().numpy()) <= 2e-2
+    assert rel_max_err(Ye.float().cpu().numpy(), _sequential(torch, X, layers).float().cpu().numpy()) <= 2e-2
     assert pyc_amd.w8a16_chain_error() == 0
 
 
