@@ -19,9 +19,10 @@
 //    row statistics need only in-lane reductions plus one exchange with the
 //    lane 32 apart, and P^T is already in the B-operand layout of the second
 //    MFMA: no shuffles of P through LDS.
-//  * Online softmax in base 2 (scores pre-multiplied by scale*log2(e)); the
-//    first key block always contains key 0, so every query's running max is
-//    finite before any fully-masked block is seen.
+//  * Online softmax in base 2 (exponents scale*log2(e)*s - m) against a
+//    per-query reference m set by the first key block (which holds key 0, so
+//    no query has all of it masked) and raised only when a later block would
+//    overflow (see v_phase).
 //  * Workgroup order is XCD-aware: ids are remapped so that one XCD walks all
 //    query blocks of a few heads at a time, keeping their K/V in its L2.
 #include <type_traits>
@@ -58,11 +59,10 @@ __device__ inline uint32_t pack2(float lo, float hi, f16_t) {
 // exp2 is the bare v_exp_f32 (its arguments here are <= 8, results that
 // underflow flush to 0, which softmax tolerates), not exp2f's range-reduced
 // sequence of five instructions.
-// Rescaling threshold of the online softmax (base-2 units): the running max
-// is only raised when a block's max exceeds it by more than this, so most
-// blocks skip the O and l rescale; probabilities then stay below 2^8 before
-// normalisation, and the final O / l is exact whichever max was used.
-constexpr float kAttnRescaleLog2 = 8.0f;
+// Bound of the softmax's common path: a lane's block sum of p (an upper
+// bound of its largest p) must stay at or below this, so P fits bf16/f16 and
+// O stays far from overflow.
+constexpr float kAttnFastSumMax = 16384.0f;
 
 constexpr int kAttnBK = 64;     // keys per LDS block
 constexpr int kAttnRing = 4;    // K/V blocks in the LDS ring
@@ -119,9 +119,6 @@ __device__ inline u32x2 lds_read_tr16(const uint16_t* p) {
     return __builtin_bit_cast(u32x2, v);
 }
 
-// POS: scale > 0, folded into the exp2 argument; otherwise scores are
-// multiplied by the scale first.
-//
 // Schedule. Each wave runs, per q-block, the phase sequence
 //   M(-1) V(-1) M(0) V(0) ... V(n-2) M(n-1)
 // with M(k) = S(k+1) = K(k+1) Q^T and O^T += V(k)^T P(k)^T (MFMA work) and
@@ -135,7 +132,7 @@ __device__ inline u32x2 lds_read_tr16(const uint16_t* p) {
 // the barriers that follow make it visible before S(j) (group 0's M(j-1)).
 // The slot's previous block, j-4, was last read by group 1's M(j-4), two
 // global phases before the earliest issue of block j.
-template <typename T, int D, bool POS>
+template <typename T, int D>
 __global__ void __launch_bounds__(kAttnWaves * kWave, 1)
 attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
                 const uint16_t* __restrict__ Vp, uint16_t* __restrict__ O, int BH, int S,
@@ -211,8 +208,6 @@ attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) k_off[kk] = l32 * D + k_swz<CH>(l32, kk * 2 + h) * 8;
 
-    const float c = POS ? scale_log2 : 1.f;
-
     for (int part = 0; part < 2; ++part) {
         int qb = u;
         if (pair) {
@@ -243,7 +238,7 @@ attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
         for (int t = 0; t < DT; ++t)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
-        float m_run = -INFINITY;  // running max (base-2 scaled) of this lane's query
+        float m_run = 0.f;  // reference exponent (base 2) of this lane's query
         float l_run = 0.f;        // running sum over the keys this lane holds
         f32x16 sc[2];             // S^T of the block the next V phase works on
         u32x4 pf[4];              // P^T fragments of the four 16-key steps of the block the next PV uses
@@ -330,15 +325,21 @@ attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
         using yes = std::true_type;
         using no = std::false_type;
 
-        // V phase: online softmax of block j (scores in sc) into pf.
+        // V phase: online softmax of block j (raw scores in sc) into pf.
+        // Block 0 (which holds key 0, so no query has all of it masked) sets
+        // each query's reference m to its exact max. Later blocks take the
+        // common path p = exp2(scale*log2(e)*s - m) with no max at all; only
+        // if some lane's block sum exceeds 2^14 (a p may exceed 2^14, or
+        // overflowed) does the wave take the slow path, which raises m to the
+        // block max (never lowers it: such a block's max is above m), scales
+        // O and l down and recomputes p. Keys far below m underflow to 0, as
+        // in any softmax against the max; O / l is exact whatever m is.
         auto v_phase = [&](int j) {
             const int key0 = j * kAttnBK;
-            if (!POS) {
 #pragma unroll
-                for (int e = 0; e < 2; ++e)
+            for (int e = 0; e < 2; ++e)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) sc[e][r] *= scale_log2;
-            }
+                for (int r = 0; r < 16; ++r) sc[e][r] = fmaf(sc[e][r], scale_log2, -m_run);
             // lane holds keys key0 + 32e + 8*(r/4) + 4h + (r%4) of query qi
             const bool edge = (causal && key0 + kAttnBK - 1 > q0) || key0 + kAttnBK > S;  // wave-uniform
             if (edge) {
@@ -354,41 +355,65 @@ attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
                         sc[e][r] = x;
                     }
             }
-            float m0 = vmax(sc[0][0], sc[0][1]), m1 = vmax(sc[1][0], sc[1][1]);
+            // p = exp2(x) into pf; returns this lane's sum of the rounded p
+            auto exponentiate = [&]() {
+                float ls[2] = {0.f, 0.f};
 #pragma unroll
-            for (int r = 2; r < 16; r += 2) {
-                m0 = vmax(vmax(m0, sc[0][r]), sc[0][r + 1]);
-                m1 = vmax(vmax(m1, sc[1][r]), sc[1][r + 1]);
+                for (int e = 0; e < 2; ++e)
+#pragma unroll
+                    for (int r = 0; r < 16; r += 2) {
+                        const float p0 = __builtin_amdgcn_exp2f(sc[e][r]);
+                        const float p1 = __builtin_amdgcn_exp2f(sc[e][r + 1]);
+                        const uint32_t pr = pack2(p0, p1, T{});
+                        pf[2 * e + (r >> 3)][(r & 7) >> 1] = pr;
+                        ls[e] = add_pair(pr, ls[e], T{});
+                    }
+                return ls[0] + ls[1];
+            };
+            // query max of the exponents (both lane halves)
+            auto block_max = [&]() {
+                float m0 = vmax(sc[0][0], sc[0][1]), m1 = vmax(sc[1][0], sc[1][1]);
+#pragma unroll
+                for (int r = 2; r < 16; r += 2) {
+                    m0 = vmax(vmax(m0, sc[0][r]), sc[0][r + 1]);
+                    m1 = vmax(vmax(m1, sc[1][r]), sc[1][r + 1]);
+                }
+                const float mh = vmax(m0, m1);
+                return vmax(mh, other_half(mh, xaddr));
+            };
+            if (j == 0) {
+                const float shift = block_max();  // finite: key 0 is never masked
+                m_run += shift;
+#pragma unroll
+                for (int e = 0; e < 2; ++e)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) sc[e][r] -= shift;
             }
-            const float mh = vmax(m0, m1);
-            const float mloc = vmax(mh, other_half(mh, xaddr)) * c;
-            // lazy rescale: only when some lane's max grew past the threshold
-            const bool grow = mloc > m_run + kAttnRescaleLog2;
-            if (__any(grow)) {
-                const float m_new = vmax(m_run, mloc);
-                // 0 while m_run = -inf (nothing accumulated yet)
-                const float alpha = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
-                m_run = m_new;
+            float lsum = exponentiate();
+            const bool bad = j != 0 && !(lsum <= kAttnFastSumMax);
+            if (__any(bad)) {
+                // both lane halves of a query move together (the PV product
+                // adds their p into one row); the partner's flag is
+                // recomputed from its sum (an exchanged 0/1 flag was folded
+                // into the lane's own by this compiler)
+                const float mrel = block_max();
+                const float lsum_o = other_half(lsum, xaddr);
+                const bool badq = bad || !(lsum_o <= kAttnFastSumMax);
+                const float shift = badq ? mrel : 0.f;  // > 0 for a bad query
+                const float alpha = __builtin_amdgcn_exp2f(-shift);
+                m_run += shift;
                 l_run *= alpha;
 #pragma unroll
                 for (int t = 0; t < DT; ++t)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) acc[t][r] *= alpha;
+#pragma unroll
+                for (int e = 0; e < 2; ++e)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) sc[e][r] -= shift;
+                lsum = exponentiate();
             }
-            // a lane whose keys so far are all masked has m_run = -inf
-            const float m_use = m_run == -INFINITY ? 0.f : m_run;
-            float ls[2] = {0.f, 0.f};
-#pragma unroll
-            for (int e = 0; e < 2; ++e)
-#pragma unroll
-                for (int r = 0; r < 16; r += 2) {
-                    const float p0 = __builtin_amdgcn_exp2f(fmaf(sc[e][r], c, -m_use));
-                    const float p1 = __builtin_amdgcn_exp2f(fmaf(sc[e][r + 1], c, -m_use));
-                    const uint32_t pr = pack2(p0, p1, T{});
-                    pf[2 * e + (r >> 3)][(r & 7) >> 1] = pr;
-                    ls[e] = add_pair(pr, ls[e], T{});
-                }
-            l_run += ls[0] + ls[1];
+            l_run += lsum;
         };
 
         issue(0);
@@ -455,10 +480,7 @@ static hipError_t launch_attn(int B, int H, int S, int causal, const void* q, co
     const int nqb = (S + bq - 1) / bq;
     const int units = (causal && nqb > 1) ? (nqb + 1) / 2 : nqb;
     const dim3 grid(BH * units), block(kAttnWaves * kWave);
-    if (scale_log2 > 0.f)
-        hipLaunchKernelGGL((attn_fwd_kernel<T, D, true>), grid, block, 0, s, qq, kk, vv, oo, BH, S, causal, scale_log2);
-    else
-        hipLaunchKernelGGL((attn_fwd_kernel<T, D, false>), grid, block, 0, s, qq, kk, vv, oo, BH, S, causal, scale_log2);
+    hipLaunchKernelGGL((attn_fwd_kernel<T, D>), grid, block, 0, s, qq, kk, vv, oo, BH, S, causal, scale_log2);
     return hipGetLastError();
 }
 

@@ -42,14 +42,17 @@ def test_attention_vs_oracle(gpu, B, H, S, D, causal):
     _check(got, ref)
 
 
-@pytest.mark.parametrize("case", ["large_logits", "growing_keys", "negative_scale", "zero_scale"])
+@pytest.mark.parametrize("case", ["large_logits", "growing_keys", "negative_scale", "zero_scale",
+                                  "all_underflow"])
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("causal", [True, False])
 def test_attention_softmax_paths(gpu, case, D, causal):
-    """Online-softmax paths: logits whose block maxima jump by far more than
-    the lazy-rescale threshold (large_logits, growing_keys: key j scaled by
-    1 + j/32 so every later block raises the max), and scales <= 0 (the
-    scale is then applied before the max instead of inside exp2)."""
+    """Online-softmax paths: logits whose block maxima jump far above the
+    current reference (large_logits, growing_keys: key j scaled by 1 + j/32 so
+    every later block raises the max), scales <= 0, and exponents that all
+    underflow against the initial reference (all_underflow: positive q.k
+    around 100 times a scale of -4, so every exp2 of the first block is 0
+    until the reference moves down to the block max)."""
     torch = gpu
     B, H, S = 1, 2, 300
     r = np.random.default_rng(len(case) * 10 + D + causal)
@@ -64,6 +67,10 @@ def test_attention_softmax_paths(gpu, case, D, causal):
         k *= (1.0 + np.arange(S, dtype=np.float32) / 32.0)[None, None, :, None]
     elif case == "negative_scale":
         scale = -0.3 / np.sqrt(D)
+    elif case == "all_underflow":
+        q = np.abs(q) + 1.0
+        k = np.abs(k) + 1.0
+        scale = -4.0
     else:
         scale = 0.0
     q, k, v = (oracle.f32_to_bf16(t) for t in (q, k, v))
