@@ -210,6 +210,49 @@ typedef struct {
     int f32_bias_needed[PYC_IR_MAX_OPS]; /* half add operand needing an fp32 device copy */
 } hip_plan;
 
+/* 1 if value v is read by no step but `reader` and is no module output. */
+static int value_private(const hip_plan* p, int v, size_t reader) {
+    size_t t, i;
+    for (t = 0; t < p->nsteps; ++t) {
+        const hip_step* st = &p->steps[t];
+        if (t == reader) {
+            continue;
+        }
+        if (st->in[0] == v || st->in[1] == v || st->in[2] == v || st->add_in == v) {
+            return 0;
+        }
+    }
+    for (i = 0; i < p->n_outputs; ++i) {
+        if (p->output_src[i] == v) {
+            return 0;
+        }
+    }
+    return 1;
+}
+
+/* Number of consecutive fp8-weight steps from step s that run as one chain
+ * launch (pyc_hip_w8a16_chain_dispatch): each reads the previous one's output,
+ * which nothing else reads, with K % 128 == 0 and N % 64 == 0 throughout.
+ * 1 when step s starts no chain. */
+#define HIP_CHAIN_MAX_STEPS 32
+static size_t w8_chain_len(const hip_plan* p, size_t s) {
+    size_t e = s;
+    const hip_step* a = &p->steps[s];
+    if (a->kind != ST_W8A16 || a->add_mode != ADD_NONE || (a->k % 128) != 0 || (a->n % 64) != 0) {
+        return 1;
+    }
+    while (e + 1 < p->nsteps && e + 1 - s < HIP_CHAIN_MAX_STEPS) {
+        const hip_step* cur = &p->steps[e];
+        const hip_step* nx = &p->steps[e + 1];
+        if (nx->kind != ST_W8A16 || nx->add_mode != ADD_NONE || nx->in[0] != cur->out || nx->m != cur->m ||
+            nx->k != cur->n || (nx->n % 64) != 0 || !value_private(p, cur->out, e + 1)) {
+            break;
+        }
+        ++e;
+    }
+    return e - s + 1;
+}
+
 static int consumers(const pyc_ir_module* m, int id, int* only) {
     size_t i, j;
     int n = 0;
@@ -728,6 +771,30 @@ static int enqueue_steps(const pyc_ir_module* m, const hip_plan* plan, char* why
     for (s = 0; s < plan->nsteps; ++s) {
         const hip_step* st = &plan->steps[s];
         void* out = g_ws.val[st->out].ptr;
+        const size_t clen = w8_chain_len(plan, s);
+        if (clen >= 2) {
+            /* the whole run of fp8-weight steps in one launch */
+            const void* wq[HIP_CHAIN_MAX_STEPS];
+            const float* sc[HIP_CHAIN_MAX_STEPS];
+            int cn[HIP_CHAIN_MAX_STEPS], ck[HIP_CHAIN_MAX_STEPS], cr[HIP_CHAIN_MAX_STEPS];
+            size_t c;
+            for (c = 0; c < clen; ++c) {
+                const hip_step* q = &plan->steps[s + c];
+                wq[c] = g_ws.val[q->in[1]].ptr;
+                sc[c] = (const float*)g_ws.val[q->in[2]].ptr;
+                cn[c] = q->n;
+                ck[c] = q->k;
+                cr[c] = q->relu;
+            }
+            if (pyc_hip_w8a16_chain_dispatch("hip_w8a16_chain_e4m3", st->m, (int)clen, g_ws.val[st->in[0]].ptr, wq,
+                                             sc, cn, ck, cr, g_ws.val[plan->steps[s + clen - 1].out].ptr,
+                                             st_stream) != 0) {
+                snprintf(why, why_cap, "hip_kernel_failed:hip_w8a16_chain_e4m3");
+                return -1;
+            }
+            s += clen - 1;
+            continue;
+        }
         int rc = -1;
         int epi = (st->relu ? PYC_HIP_EPI_RELU : 0);
         const float* bias = NULL;
@@ -932,7 +999,17 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
         if (use_graph) {
             /* the fp8 GEMM's split-K workspace cannot be allocated inside a capture */
             for (i = 0; i < plan.nsteps; ++i) {
-                if (plan.steps[i].kind == ST_W8A16) {
+                const size_t clen = w8_chain_len(&plan, i);
+                if (clen >= 2) {
+                    int cn[HIP_CHAIN_MAX_STEPS], ck[HIP_CHAIN_MAX_STEPS];
+                    size_t c;
+                    for (c = 0; c < clen; ++c) {
+                        cn[c] = plan.steps[i + c].n;
+                        ck[c] = plan.steps[i + c].k;
+                    }
+                    (void)pyc_hip_w8a16_chain_reserve(plan.steps[i].m, (int)clen, cn, ck);
+                    i += clen - 1;
+                } else if (plan.steps[i].kind == ST_W8A16) {
                     (void)pyc_hip_w8a16_reserve(plan.steps[i].n, plan.steps[i].k);
                 }
             }
@@ -1036,7 +1113,7 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
         const char* sym = NULL;
         for (i = 0; i < plan.nsteps; ++i) {
             if (plan.steps[i].kind == ST_GEMM || plan.steps[i].kind == ST_W8A16) {
-                sym = plan.steps[i].symbol;
+                sym = w8_chain_len(&plan, i) >= 2 ? "hip_w8a16_chain_e4m3" : plan.steps[i].symbol;
                 break;
             }
         }

@@ -124,9 +124,42 @@ def test_decode_chain_module_fp8():
     st, (out,), s = mdl.run(ins, [(M, D)], in_dtypes=dts, out_dtypes=[abi.DTYPE_BF16], out_np_dtype=np.uint16)
     mdl.close()
     assert st == 0
-    assert "hip_gemm_w8a16_e4m3" in _native(s)
+    # four fp8 steps, each feeding only the next: one chain launch
+    assert "hip_w8a16_chain_e4m3" in _native(s)
     ref = oracle.bf16_to_f32(oracle.w8a16_chain(x, layers))
     assert rel_max_err(oracle.bf16_to_f32(out), ref) <= 2e-2
+
+
+def test_decode_layer_hidden_output_not_chained():
+    """An fp8 up/down layer whose hidden activation is also a module output:
+    the two GEMMs must not be fused into one chain launch (the chain keeps its
+    intermediates private), and both outputs must match the oracle."""
+    M, D, F = 16, 256, 384
+    r = np.random.default_rng(4)
+    x = oracle.f32_to_bf16(r.standard_normal((M, D)).astype(np.float32))
+    wu, su = oracle.quantize_e4m3_per_col((r.standard_normal((D, F)) * np.sqrt(2 / D)).astype(np.float32))
+    wd, sd = oracle.quantize_e4m3_per_col((r.standard_normal((F, D)) * np.sqrt(2 / F)).astype(np.float32))
+    ops = [eu.op(abi.OP_INPUT, "x", (M, D), dtype=abi.DTYPE_BF16),
+           eu.op(abi.OP_INPUT, "wu", (F, D), dtype=abi.DTYPE_FP8_E4M3), eu.op(abi.OP_INPUT, "su", (F,)),
+           eu.op(abi.OP_INPUT, "wd", (D, F), dtype=abi.DTYPE_FP8_E4M3), eu.op(abi.OP_INPUT, "sd", (D,)),
+           eu.op(abi.OP_MATMUL, "up", (), (0, 1, 2), dtype=abi.DTYPE_BF16),
+           eu.op(abi.OP_RELU, "relu", (), (5,), dtype=abi.DTYPE_BF16),
+           eu.op(abi.OP_MATMUL, "down", (), (6, 3, 4), dtype=abi.DTYPE_BF16),
+           eu.op(abi.OP_OUTPUT, "h", (M, F), (6,), dtype=abi.DTYPE_BF16),
+           eu.op(abi.OP_OUTPUT, "y", (M, D), (7,), dtype=abi.DTYPE_BF16)]
+    mdl = eu.Model(eu.mine(), ops, backend=abi.BACKEND_CUDA)
+    assert mdl.status == 0
+    dts = [abi.DTYPE_BF16, abi.DTYPE_FP8_E4M3, abi.DTYPE_F32, abi.DTYPE_FP8_E4M3, abi.DTYPE_F32]
+    st, (h, y), s = mdl.run([x, wu, su, wd, sd], [(M, F), (M, D)], in_dtypes=dts,
+                            out_dtypes=[abi.DTYPE_BF16, abi.DTYPE_BF16], out_np_dtype=np.uint16)
+    mdl.close()
+    assert st == 0
+    reason = _native(s)
+    assert "hip_gemm_w8a16_e4m3" in reason and "chain" not in reason
+    h_ref = oracle.w8a16_layer(x, wu, su, True)
+    y_ref = oracle.w8a16_layer(h_ref, wd, sd, False)
+    assert rel_max_err(oracle.bf16_to_f32(h), oracle.bf16_to_f32(h_ref)) <= 2e-2
+    assert rel_max_err(oracle.bf16_to_f32(y), oracle.bf16_to_f32(y_ref)) <= 2e-2
 
 
 def test_conv_and_attention_modules():
