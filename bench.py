@@ -326,8 +326,11 @@ WORKLOADS = {"gemm_bf16": wl_gemm_bf16, "gemm_f32_cfg1": wl_gemm_f32_cfg1, "deco
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=100)
+    # The GPU clock of an idle card ramps up over the first tens of
+    # milliseconds of load: 10 warmup launches left the attention kernel's
+    # timed steps 20% slow. 100 launches cover the ramp for every workload.
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--workload", default="gemm_bf16", choices=sorted(WORKLOADS))
     ap.add_argument("--symbol", default=None, help="GEMM kernel symbol override")
     ap.add_argument("--cpu-rows", type=int, default=1024,

@@ -96,15 +96,12 @@ __device__ inline float vmax(float a, float b) { return __builtin_elementwise_ma
 __device__ inline float other_half(float x, int xaddr) {
     return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(xaddr, __builtin_bit_cast(int, x)));
 }
-// acc + lo + hi of a packed pair of probabilities (one v_dot2c_f32_{bf16,f16}):
-// the row sum is taken over the rounded values the PV product uses.
-__device__ inline float add_pair(uint32_t pr, float acc, bf16_t) {
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pr), bf16x2_t{(__bf16)1.f, (__bf16)1.f}, acc,
-                                           false);
-}
-__device__ inline float add_pair(uint32_t pr, float acc, f16_t) {
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, pr), f16x2_t{(_Float16)1.f, (_Float16)1.f}, acc, false);
-}
+// The row sums of p are plain fp32 adds of the unrounded p. A v_dot2c of the
+// rounded pair with (1, 1) would take one instruction per pair instead of
+// two, but on gfx950 the dot instructions wait behind the matrix unit: while
+// the SIMD's other wave runs MFMAs, a v_dot2c_f32_bf16 issues about every
+// 37 cycles against about 7 for a v_add_f32 (measured), which made the
+// softmax phase the slower one of the pair.
 
 // LDS transpose read (gfx950 ds_read_b64_tr_b16): within each group of 16
 // lanes, lane i receives element (i & 3) of the 8 bytes that lane
@@ -119,19 +116,34 @@ __device__ inline u32x2 lds_read_tr16(const uint16_t* p) {
     return __builtin_bit_cast(u32x2, v);
 }
 
-// Schedule. Each wave runs, per q-block, the phase sequence
-//   M(-1) V(-1) M(0) V(0) ... V(n-2) M(n-1)
-// with M(k) = S(k+1) = K(k+1) Q^T and O^T += V(k)^T P(k)^T (MFMA work) and
-// V(k) = softmax of S(k+1) into P(k+1) (VALU work), and a workgroup barrier
-// after every phase. Group 1 (waves 4..7) passes one extra barrier first, so
-// it runs one phase behind group 0: while a wave of one group is in an M
-// phase, the wave of the other group on the same SIMD is in a V phase, and
-// the MFMA unit and the VALU work at the same time.
-// K/V block j goes into ring slot j % 4. Every wave issues its part of block
-// j at the start of its phase M(j-3) and waits for it at the end of M(j-2);
-// the barriers that follow make it visible before S(j) (group 0's M(j-1)).
-// The slot's previous block, j-4, was last read by group 1's M(j-4), two
-// global phases before the earliest issue of block j.
+// Work. A unit is, with a causal mask, the pair of q-blocks nqb-1-u and u of
+// one head (equal work for every unit), else one q-block; each q-block is a
+// "part". The grid is persistent (at most one workgroup per CU): workgroup b
+// takes units b, b + G, b + 2G, ... (G = grid size), and the unit index is
+// remapped so that each XCD walks a contiguous range of heads, whose units
+// then share K/V in that XCD's L2.
+//
+// Schedule. The K/V blocks of all parts of a workgroup form one list: part p
+// contributes its n_p blocks and one dummy entry (a reload of its last
+// block, finite data that the unused S of the part's last M phase reads).
+// Each wave runs one phase sequence over all its parts,
+//   M(-1) V(-1) M(0) V(0) ... M(n-2) V(n-2) M(n-1) F   (per part)
+// with M(k) = S(k+1) = K(k+1) Q^T and O^T += V(k)^T P(k)^T (MFMA work), V(k) =
+// softmax of S(k+1) into P(k+1) (VALU work), F = the part's output (VALU
+// and stores), and a workgroup barrier after every phase. Group 1 (waves
+// 4..7) passes one extra barrier first, so it runs one phase behind group 0:
+// while a wave of one group is in an M phase, the wave of the other group on
+// the same SIMD is in a V or F phase, and the MFMA unit and the VALU work at
+// the same time.
+// List entry e goes into ring slot e % 4. The M phase that computes S of
+// entry e issues the wave's part of entry e + 2 (two entries were issued
+// before the first phase) and waits for entry e + 1 at its end; the barriers
+// that follow make it visible before group 0's next M phase. The slot's
+// previous entry, e - 2, was last read by group 1's M phase of entry e - 1,
+// two global phases before. The issue cursor runs into the next part, so
+// its first blocks load during the current part's last phases; the next
+// part's Q is loaded in its last V phase and waited for with the K/V of the
+// following M phase.
 template <typename T, int D>
 __global__ void __launch_bounds__(kAttnWaves * kWave, 1)
 attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
@@ -146,9 +158,11 @@ attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
     constexpr int KK = D / 16;                       // k-steps of 16 over d for S
     constexpr int TILE = kAttnBK * D;                // elements of one K or V block
     static_assert(DMAS * NT == kAttnBK * CH, "K/V split");
-    static_assert(KK % DT == 0 || DT % 1 == 0, "");
 
     __shared__ __attribute__((aligned(1024))) uint16_t smem[kAttnRing * 2 * TILE];
+    // output staging of the F phase, one area per SIMD: waves w and w + 4
+    // (the two groups) never run F at the same time
+    __shared__ __attribute__((aligned(1024))) uint16_t ostage[kAttnWaves / 2][32 * D];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -158,24 +172,46 @@ attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
     const int h = lane >> 5;
     const int xaddr = (lane ^ 32) * 4;  // ds_bpermute address of the lane 32 apart
 
-    // Work units: with a causal mask, unit u of a head is the pair of
-    // q-blocks nqb-1-u and u (equal total work for every unit); otherwise
-    // one q-block. Unit order is XCD-aware: each XCD gets a contiguous range
-    // of heads, so the units of one head share K/V in that XCD's L2.
     const int nqb = (S + BQ - 1) / BQ;
     const bool pair = causal && nqb > 1;
     const int units = pair ? (nqb + 1) / 2 : nqb;
     const int total = units * BH;
-    int w = blockIdx.x;
-    if ((total & 7) == 0) w = (w & 7) * (total >> 3) + (w >> 3);
-    const int bh = w / units;
-    const int u = w - bh * units;
-    const size_t base = (size_t)bh * S * D;
+    const int G = (int)gridDim.x;
+    const uint32_t head_bytes = (uint32_t)((size_t)S * D * 2);
 
-    // K/V blocks move global -> LDS by buffer_load ... lds; the descriptors
-    // cover this head only, so rows past S read as zeros.
-    const i32x4 krs = make_buf_rsrc(Kp + base, (uint32_t)((size_t)S * D * 2));
-    const i32x4 vrs = make_buf_rsrc(Vp + base, (uint32_t)((size_t)S * D * 2));
+    // Part cursor (wave-uniform): round i of this workgroup (i < 0 once the
+    // list is exhausted), which part of the unit, head, q-block, K/V blocks.
+    struct Cursor {
+        int i, sec, bh, qb, n;
+    };
+    auto nblocks = [&](int qb) {
+        const int kend = causal ? min(qb * BQ + BQ, S) : S;
+        return (kend + kAttnBK - 1) / kAttnBK;
+    };
+    auto first_of = [&](int i, Cursor& c) {
+        int w = i * G + (int)blockIdx.x;
+        if (w >= total) {
+            c.i = -1;
+            return;
+        }
+        if ((total & 7) == 0) w = (w & 7) * (total >> 3) + (w >> 3);
+        c.i = i;
+        c.sec = 0;
+        c.bh = w / units;
+        const int u = w - c.bh * units;
+        c.qb = pair ? nqb - 1 - u : u;
+        c.n = nblocks(c.qb);
+    };
+    auto advance = [&](Cursor& c) {
+        if (pair && c.sec == 0 && nqb - 1 - c.qb != c.qb) {
+            c.sec = 1;
+            c.qb = nqb - 1 - c.qb;
+            c.n = nblocks(c.qb);
+            return;
+        }
+        first_of(c.i + 1, c);
+    };
+
     const uint32_t lds0 = (uint32_t)(uintptr_t)&smem[0];
     uint32_t kvo[DMAS], vvo[DMAS], klds[DMAS];
 #pragma unroll
@@ -186,6 +222,40 @@ attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
         vvo[j] = (uint32_t)((row * CH + v_swz<CH>(row, p)) * 16);
         klds[j] = __builtin_amdgcn_readfirstlane(lds0 + (uint32_t)((j * kAttnWaves + wave) * ROWS_PER_DMA * D * 2));
     }
+
+    // Issue cursor: K/V blocks move global -> LDS by buffer_load ... lds. The
+    // descriptors cover one head only, so rows past S read as zeros. The
+    // block offset goes into the per-lane offset (not the scalar one) so that
+    // the range check sees the whole offset of rows past S. A dummy entry
+    // (and every issue after the last part) reloads the previous block into
+    // its free slot, so that every M phase issues the same number of loads.
+    Cursor ic;
+    first_of(0, ic);
+    int ie = 0;           // entry of ic's list, 0..ic.n (ic.n is the dummy)
+    uint32_t inext = 0;   // list index of the next issue
+    uint32_t iboff = 0;
+    i32x4 ikrs, ivrs;
+    auto set_issue_head = [&]() {
+        const size_t b = (size_t)ic.bh * S * D;
+        ikrs = make_buf_rsrc(Kp + b, head_bytes);
+        ivrs = make_buf_rsrc(Vp + b, head_bytes);
+    };
+    set_issue_head();  // the grid is no larger than the number of units
+    auto issue_next = [&]() {
+        if (ic.i >= 0 && ie < ic.n) iboff = (uint32_t)ie * kAttnBK * D * 2;
+        const uint32_t sb = (inext % kAttnRing) * 2 * TILE * 2;
+#pragma unroll
+        for (int jj = 0; jj < DMAS; ++jj) {
+            lds_dma_buf_b128(ikrs, kvo[jj] + iboff, 0u, klds[jj] + sb);
+            lds_dma_buf_b128(ivrs, vvo[jj] + iboff, 0u, klds[jj] + sb + TILE * 2);
+        }
+        ++inext;
+        if (ic.i >= 0 && ++ie > ic.n) {
+            advance(ic);
+            ie = 0;
+            if (ic.i >= 0) set_issue_head();
+        }
+    };
 
     // Per-lane LDS element offsets of the fragment reads. The K rows a lane
     // reads differ by multiples of 32 and the V rows by multiples of 8, while
@@ -208,68 +278,67 @@ attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) k_off[kk] = l32 * D + k_swz<CH>(l32, kk * 2 + h) * 8;
 
-    for (int part = 0; part < 2; ++part) {
-        int qb = u;
-        if (pair) {
-            qb = part == 0 ? nqb - 1 - u : u;
-            if (part == 1 && qb == nqb - 1 - u) break;
-        } else if (part == 1) {
-            break;
-        }
-        if (part == 1) __syncthreads();  // every wave is done with the previous q-block's ring
+    // Q fragments (B operand of S^T = K Q^T): lane holds Q[qi][kk*16 + 8h .. +8].
+    // Lanes of queries past S load row S-1 (finite scores for queries that
+    // are never stored); no select, so no register write that would have to
+    // wait for the loads still in flight.
+    auto load_q = [&](const Cursor& c, u32x4* q) {
+        const int qi = min(c.qb * BQ + wave * 32 + l32, S - 1);
+        const uint16_t* src = Q + (size_t)c.bh * S * D + (size_t)qi * D + h * 8;
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) q[kk] = *reinterpret_cast<const u32x4*>(src + kk * 16);
+    };
 
-        const int q0 = qb * BQ + wave * 32;  // this wave's first query
-        const int qi = q0 + l32;             // this lane's query
-        const int q_last = min(qb * BQ + BQ, S) - 1;
-        const int kend = causal ? q_last + 1 : S;
-        const int n = (kend + kAttnBK - 1) / kAttnBK;
+    Cursor cc;
+    first_of(0, cc);
+    u32x4 qf[KK], qn[KK];
+    load_q(cc, qf);
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) qn[kk] = u32x4{0, 0, 0, 0};
+    f32x16 acc[DT];
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
+    float m_run = 0.f;  // reference exponent (base 2) of this lane's query
+    float l_run = 0.f;  // running sum over the keys this lane holds
+    f32x16 sc[2];       // S^T of the block the next V phase works on
+    u32x4 pf[4];        // P^T fragments of the four 16-key steps of the block the next PV uses
+    uint32_t e0 = 0;    // list index of the current part's block 0
+
+    issue_next();
+    issue_next();
+    wait_vmem_le<2 * DMAS>();       // own part of entry 0 landed ...
+    // The compiler does not see the LDS-DMA loads (inline asm) and waits for
+    // every load still in flight before the first use of Q registers; the
+    // empty asm takes that wait here, once, rather than in the first M phase
+    // of every part (where it would wait for the block that phase just issued).
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) asm volatile("" : "+v"(qf[kk]));
+    __syncthreads();                // ... and every wave's
+    if (grp == 1) __syncthreads();  // group 1 runs one phase behind
+    while (cc.i >= 0) {
+        const int q0 = cc.qb * BQ + wave * 32;  // this wave's first query
+        const int qi = q0 + l32;                // this lane's query
+        const int n = cc.n;
         // blocks past this wave's diagonal are fully masked for it
         const int n_w = causal ? min(n, (q0 + 31) / kAttnBK + 1) : n;
+        Cursor nc = cc;
+        advance(nc);
 
-        // Q fragments (B operand of S^T = K Q^T): lane holds Q[qi][kk*16 + 8h .. +8].
-        u32x4 qf[KK];
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk) {
-            qf[kk] = qi < S ? *reinterpret_cast<const u32x4*>(Q + base + (size_t)qi * D + kk * 16 + h * 8)
-                            : u32x4{0, 0, 0, 0};
-        }
-        f32x16 acc[DT];
-#pragma unroll
-        for (int t = 0; t < DT; ++t)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
-        float m_run = 0.f;  // reference exponent (base 2) of this lane's query
-        float l_run = 0.f;        // running sum over the keys this lane holds
-        f32x16 sc[2];             // S^T of the block the next V phase works on
-        u32x4 pf[4];              // P^T fragments of the four 16-key steps of the block the next PV uses
-
-        // The block offset goes into the per-lane offset (not the scalar one)
-        // so that the descriptor's range check sees the whole offset of rows
-        // past S. Blocks past the last are clamped to it (a harmless reload
-        // into a free slot) so that every phase issues the same loads.
-        auto issue = [&](int j) {
-            const uint32_t boff = (uint32_t)min(j, n - 1) * kAttnBK * D * 2;
-            const uint32_t sb = (uint32_t)(j % kAttnRing) * 2 * TILE * 2;
-#pragma unroll
-            for (int jj = 0; jj < DMAS; ++jj) {
-                lds_dma_buf_b128(krs, kvo[jj] + boff, 0u, klds[jj] + sb);
-                lds_dma_buf_b128(vrs, vvo[jj] + boff, 0u, klds[jj] + sb + TILE * 2);
-            }
-        };
-
-        // M phase: S of block js (if DS) and PV of block jp (if DP), interleaved;
-        // the flags are compile-time so that the body is straight-line code.
-        // Step st does the two S MFMAs of k-step st and NPV of the 4*DT PV
-        // MFMAs; the fragments of step st+1 are read from LDS while the MFMAs
-        // of step st run.
+        // M phase: S of list entry es (if DS) and PV of entry ep (if DP),
+        // interleaved; the flags are compile-time so that the body is
+        // straight-line code. Step st does the two S MFMAs of k-step st and
+        // NPV of the 4*DT PV MFMAs; the fragments of step st+1 are read from
+        // LDS while the MFMAs of step st run.
         constexpr int NPV = (4 * DT) / KK;
         static_assert(NPV * KK == 4 * DT, "PV steps per S step");
-        auto m_phase = [&](auto ds_tag, auto dp_tag, int js, int jp) {
+        auto m_phase = [&](auto ds_tag, auto dp_tag, uint32_t es, uint32_t ep) {
             constexpr bool DS = decltype(ds_tag)::value, DP = decltype(dp_tag)::value;
             // slot offsets made opaque so that the per-slot fragment
             // addresses are formed here (one add each) instead of being
             // hoisted out of the loop for all four slots (which costs VGPRs)
-            uint32_t so_s = (uint32_t)(js % kAttnRing) * 2 * TILE, so_p = (uint32_t)(jp % kAttnRing) * 2 * TILE + TILE;
+            uint32_t so_s = (es % kAttnRing) * 2 * TILE, so_p = (ep % kAttnRing) * 2 * TILE + TILE;
             asm volatile("" : "+s"(so_s), "+s"(so_p));
             const uint16_t* ks = smem + so_s;
             const uint16_t* vs = smem + so_p;
@@ -355,20 +424,22 @@ attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
                         sc[e][r] = x;
                     }
             }
-            // p = exp2(x) into pf; returns this lane's sum of the rounded p
+            // p = exp2(x) into pf; returns this lane's sum of p in fp32 (of p
+            // before rounding to T: it differs from the sum of the rounded p
+            // by at most half a unit in T's last place, relative)
             auto exponentiate = [&]() {
-                float ls[2] = {0.f, 0.f};
+                float ls[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int e = 0; e < 2; ++e)
 #pragma unroll
                     for (int r = 0; r < 16; r += 2) {
                         const float p0 = __builtin_amdgcn_exp2f(sc[e][r]);
                         const float p1 = __builtin_amdgcn_exp2f(sc[e][r + 1]);
-                        const uint32_t pr = pack2(p0, p1, T{});
-                        pf[2 * e + (r >> 3)][(r & 7) >> 1] = pr;
-                        ls[e] = add_pair(pr, ls[e], T{});
+                        pf[2 * e + (r >> 3)][(r & 7) >> 1] = pack2(p0, p1, T{});
+                        ls[2 * e] += p0;
+                        ls[2 * e + 1] += p1;
                     }
-                return ls[0] + ls[1];
+                return (ls[0] + ls[1]) + (ls[2] + ls[3]);
             };
             // query max of the exponents (both lane halves)
             auto block_max = [&]() {
@@ -416,11 +487,6 @@ attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
             l_run += lsum;
         };
 
-        issue(0);
-        issue(1);
-        wait_vmem_le<2 * DMAS>();  // own part of block 0 landed ...
-        __syncthreads();           // ... and every wave's
-        if (grp == 1) __syncthreads();  // group 1 runs one phase behind
         for (int k = -1; k < n; ++k) {
             // M(k): S(k+1), PV(k). The wave in its M phase gets the higher
             // issue priority: its MFMAs then go out as soon as the matrix
@@ -428,43 +494,103 @@ attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
             // the remaining issue cycles (left to age order, the older
             // group's softmax would delay the younger group's MFMAs).
             __builtin_amdgcn_s_setprio(2);
-            issue(k + 3);
+            issue_next();
             // wave-uniform. The last PV of a wave (k = n_w - 1) also computes
             // an S that is never used: its slot holds finite data (a real
-            // block, or the clamped reload of block n-1), and one variant
-            // fewer keeps the register allocation tight.
-            if (k < 0) m_phase(yes{}, no{}, k + 1, k);
-            else if (k < n_w) m_phase(yes{}, yes{}, k + 1, k);
-            wait_vmem_le<2 * DMAS>();  // own part of block k+2 landed
+            // block or a dummy entry), and one variant fewer keeps the
+            // register allocation tight.
+            if (k < 0) m_phase(yes{}, no{}, e0, e0);
+            else if (k < n_w) m_phase(yes{}, yes{}, e0 + (uint32_t)(k + 1), e0 + (uint32_t)k);
+            wait_vmem_le<2 * DMAS>();  // own part of the next entry (and any Q prefetch) landed
             __builtin_amdgcn_s_setprio(0);
             __syncthreads();
             if (k + 1 < n) {
-                // V(k): softmax of block k+1
+                // V(k): softmax of block k+1; the last one also loads the next part's Q
+                if (k + 2 == n && nc.i >= 0) load_q(nc, qn);
                 if (k + 1 < n_w) v_phase(k + 1);
                 __syncthreads();
             }
         }
-        if (grp == 0) __syncthreads();
-        wait_vmem_le<0>();  // no LDS-DMA write may still be pending
 
-        // finalize: the row sum is split over the two lane halves
+        // F: this part's output. The next part's Q is taken first (the
+        // compiler's wait for it lands here, while the other group's M phase
+        // runs, and before the stores below, which it would also wait for).
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) asm volatile("" : "+v"(qn[kk]));
+        // The row sum is split over the two lane halves. A lane holds 8-byte
+        // pieces of its query's row; they go through LDS so that the global
+        // stores write whole rows (a direct store would touch 32 rows per
+        // instruction). Staging layout: row r (query q0 + r) of D elements,
+        // 8-byte slot s stored at slot s ^ (2 A(r) | B(r)): 16-byte chunk c at
+        // c ^ A(r), its halves swapped if B(r). For D=128, A = r % 16 and
+        // B = (r / 16) % 2: the 32 lanes of a write pass (32 rows, one slot)
+        // and the 16 lanes of a read pass (one row, 16 chunks) each touch
+        // every bank once. For D=64 (two rows per bank line), A = (r / 2) % 8
+        // and B = 0 (two-way conflicts on the writes).
         const float l_tot = l_run + other_half(l_run, xaddr);
         const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-        if (qi < S) {
-            uint16_t* orow = O + base + (size_t)qi * D;
+        {
+            constexpr int NC = D / 8;  // 16-byte chunks per row
+            auto swz_a = [](int r) { return D == 128 ? (r & 15) : ((r >> 1) & 7); };
+            auto swz_b = [](int r) { return D == 128 ? ((r >> 4) & 1) : 0; };
+            uint16_t* st = ostage[wave % (kAttnWaves / 2)];
+            // lane index made opaque here, so that the per-lane staging
+            // addresses are formed in this phase instead of being hoisted out
+            // of the part loop (where they would hold VGPRs for its duration)
+            int ln = lane;
+            asm volatile("" : "+v"(ln));
+            const int r_w = ln & 31, x_w = (2 * swz_a(r_w) | swz_b(r_w)) ^ (ln >> 5);
 #pragma unroll
             for (int t = 0; t < DT; ++t) {
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
-                    const int d = t * 32 + 8 * g + 4 * h;  // rows 8g + 4h + 0..3 of the d tile
+                    // d = t*32 + 8g + 4h .. +3: 8-byte slot 8t + 2g + h of row l32
+                    const int slot = (8 * t + 2 * g) ^ x_w;
                     u32x2 v;
                     v[0] = pack2(acc[t][4 * g + 0] * inv, acc[t][4 * g + 1] * inv, T{});
                     v[1] = pack2(acc[t][4 * g + 2] * inv, acc[t][4 * g + 3] * inv, T{});
-                    *reinterpret_cast<u32x2*>(orow + d) = v;
+                    *reinterpret_cast<u32x2*>(st + r_w * D + slot * 4) = v;
                 }
             }
+            constexpr int RPI = kWave / NC;  // rows per read instruction
+            uint16_t* obase = O + (size_t)cc.bh * S * D;
+#pragma unroll
+            for (int i = 0; i < 32 / RPI; ++i) {
+                const int r = i * RPI + ln / NC, c = ln % NC;
+                u32x4 v = *reinterpret_cast<const u32x4*>(st + r * D + (c ^ swz_a(r)) * 8);
+                if (D == 128 && i * RPI >= 16) v = u32x4{v[2], v[3], v[0], v[1]};  // B(r) = 1 for these rows
+                if (q0 + r < S) *reinterpret_cast<u32x4*>(obase + (size_t)(q0 + r) * D + c * 8) = v;
+            }
         }
+        e0 += (uint32_t)n + 1;
+        cc = nc;
+        if (cc.i >= 0) {
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) qf[kk] = qn[kk];
+#pragma unroll
+            for (int t = 0; t < DT; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
+            m_run = 0.f;
+            l_run = 0.f;
+        }
+        __syncthreads();
     }
+    if (grp == 0) __syncthreads();
+    wait_vmem_le<0>();  // no LDS-DMA write may still be pending
+}
+
+static int attn_cu_count() {
+    static int n = 0;
+    if (n == 0) {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
+            n = cus;
+        else
+            n = 256;
+    }
+    return n;
 }
 
 template <typename T, int D>
@@ -479,7 +605,14 @@ static hipError_t launch_attn(int B, int H, int S, int causal, const void* q, co
     const int bq = kAttnWaves * 32;
     const int nqb = (S + bq - 1) / bq;
     const int units = (causal && nqb > 1) ? (nqb + 1) / 2 : nqb;
-    const dim3 grid(BH * units), block(kAttnWaves * kWave);
+    const int total = BH * units;
+    if (total == 0) return hipSuccess;
+    // persistent grid: at most one workgroup per CU (the LDS ring allows no
+    // more), every workgroup the same number of rounds but the last
+    const int rounds = (total + attn_cu_count() - 1) / attn_cu_count();
+    int G = (total + rounds - 1) / rounds;
+    if (G % 8 != 0 && G > 8) G = min(total, (G + 7) / 8 * 8);
+    const dim3 grid(G), block(kAttnWaves * kWave);
     hipLaunchKernelGGL((attn_fwd_kernel<T, D>), grid, block, 0, s, qq, kk, vv, oo, BH, S, causal, scale_log2);
     return hipGetLastError();
 }
