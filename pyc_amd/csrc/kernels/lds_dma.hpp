@@ -12,10 +12,13 @@ namespace pyc {
 // vmcnt(0) wait after each issue and serialise the loads with the MFMAs); the
 // kernels wait for these loads themselves, before the barrier that publishes
 // them. M0 carries the wave-uniform LDS base; nothing else here uses M0.
+// The s_nop is the one wait state the GFX9 family requires between an SALU
+// write of M0 and an LDS-DMA load that reads it (the compiler inserts it for
+// its own code, not inside inline asm).
 // Offsets at or past the descriptor's byte count read zero.
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 __device__ inline void lds_dma_buf_b128(i32x4 rsrc, uint32_t voff, uint32_t soff, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                  :
                  : "s"(lds_base), "v"(voff), "s"(rsrc), "s"(soff)
                  : "memory", "m0");
