@@ -119,3 +119,48 @@ def test_attention_f16_and_reference_abi(gpu):
     _check(O.float().cpu().numpy(), ref)
     assert L.pyc_cutlass_attention_dispatch(b"cutlass_attention_f16", S, 96, Q.data_ptr(), K.data_ptr(),
                                             V.data_ptr(), O.data_ptr(), 0.1, s) == -1
+
+
+@pytest.mark.parametrize("B,H,S,D,causal", [
+    (4, 150, 300, 128, True),    # 600 units: every workgroup streams three rounds of one-part units
+    (2, 160, 700, 128, True),    # nqb = 3: pairs (2, 0) and the middle q-block alone; 640 units
+    (3, 100, 520, 64, False),    # non-causal, 3 q-blocks per head, 900 units
+    (1, 300, 1100, 128, True),   # nqb = 5, ragged last q-block, 900 units with 1 or 2 parts
+])
+def test_attention_persistent_rounds(gpu, B, H, S, D, causal):
+    """More units than CUs, so each workgroup of the persistent grid streams
+    several units (and their q-blocks) through one K/V ring: the hand-over
+    from one part to the next (the next part's Q and first blocks loaded
+    during the current part's tail) and from one head to another. Heads from
+    the first, middle and last units of the grid are checked against the
+    oracle; every head against O[:, :, 0] = V[:, :, 0] (causal)."""
+    torch = gpu
+    gens = [torch.Generator(device="cuda").manual_seed(s) for s in (11, 12, 13)]
+    Q, K, V = (torch.randn((B, H, S, D), generator=g, device="cuda").to(torch.bfloat16) for g in gens)
+    O = torch.empty_like(Q)
+    scale = 1.0 / np.sqrt(D)
+    pyc_amd.attention("hip_attention_bf16", Q, K, V, O, causal, scale)
+    torch.cuda.synchronize()
+    picks = {(0, 0), (B - 1, H - 1), (B // 2, H // 2), (0, H - 1), (B - 1, 1)}
+    for b, h in sorted(picks):
+        q, k, v = (oracle.bf16_to_f32(host_bits16(t[b:b + 1, h:h + 1])) for t in (Q, K, V))
+        ref = oracle.attention_f32(q, k, v, causal, scale)
+        _check(oracle.bf16_to_f32(host_bits16(O[b:b + 1, h:h + 1])), ref)
+    if causal:
+        torch.testing.assert_close(O[:, :, 0].float(), V[:, :, 0].float(), rtol=2 ** -7, atol=1e-3)
+
+
+def test_attention_f16_persistent_rounds(gpu):
+    """The f16 instantiation across several rounds per workgroup."""
+    torch = gpu
+    B, H, S, D = 2, 200, 600, 128
+    g = torch.Generator(device="cuda").manual_seed(21)
+    Q, K, V = (torch.randn((B, H, S, D), generator=g, device="cuda").to(torch.float16) for _ in range(3))
+    O = torch.empty_like(Q)
+    scale = 1.0 / np.sqrt(D)
+    pyc_amd.attention("hip_attention_f16", Q, K, V, O, True, scale)
+    torch.cuda.synchronize()
+    for b, h in [(0, 0), (1, 199), (1, 77)]:
+        q, k, v = (t[b:b + 1, h:h + 1].float().cpu().numpy() for t in (Q, K, V))
+        ref = oracle.attention_f32(q, k, v, True, scale)
+        _check(O[b:b + 1, h:h + 1].float().cpu().numpy(), ref)
