@@ -28,7 +28,18 @@
  * matmuls therefore stay on the GPU and are captured into one hipGraph.
  * Reasons of successful native runs keep the reference's prefixes:
  *   hip_native_graph_capture / hip_native_graph_replay / hip_native
- * plus ":<gemm symbol>" of the first GEMM step when there is one. */
+ * plus ":<gemm symbol>" of the first GEMM step when there is one.
+ *
+ * Device-resident tensors (an extension; the reference takes host pointers
+ * only, compiler_api.h:83-88): a pyc_tensor whose data is device memory (by
+ * hipPointerGetAttributes) is bound to the plan as it is - an input is read in
+ * place, an output is written by its producing step (or by a device copy when
+ * its value is an input or another output) - with no staging and no host
+ * copies; host and device tensors may be mixed. Such a run waits for the
+ * whole device first (the tensors may come from work on any stream), its
+ * graph signature includes the device addresses, and it is never handed to
+ * the simulated or CPU executor (which read host memory): a run that cannot
+ * go native fails with reason "device_tensors_no_cpu_fallback". */
 #include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -754,6 +765,38 @@ static float f16_bits_to_f32(uint16_t h) {
 
 /* ---------------------------------------------------------------- execution */
 
+/* 1 when p is device (or managed) memory, 0 for host memory, pageable or
+ * pinned. Tensors in device memory are bound to the plan directly: no
+ * staging, no copies (the caller keeps its tensors resident). */
+static int is_device_ptr(const void* p) {
+    hipPointerAttribute_t a;
+    if (!p) {
+        return 0;
+    }
+    if (hipPointerGetAttributes(&a, p) != hipSuccess) {
+        (void)hipGetLastError(); /* an unregistered host pointer leaves an error behind */
+        return 0;
+    }
+    return a.type == hipMemoryTypeDevice || a.type == hipMemoryTypeManaged;
+}
+
+/* Any input or output tensor in device memory (the CPU executor cannot take them). */
+static int any_device_tensor(const pyc_tensor* inputs, size_t input_count, const pyc_tensor* outputs,
+                             size_t output_count) {
+    size_t i;
+    for (i = 0; i < input_count; ++i) {
+        if (is_device_ptr(inputs[i].data)) {
+            return 1;
+        }
+    }
+    for (i = 0; i < output_count; ++i) {
+        if (is_device_ptr(outputs[i].data)) {
+            return 1;
+        }
+    }
+    return 0;
+}
+
 static uint64_t fnv(uint64_t h, const void* p, size_t n) {
     const unsigned char* c = (const unsigned char*)p;
     size_t i;
@@ -764,13 +807,14 @@ static uint64_t fnv(uint64_t h, const void* p, size_t n) {
     return h;
 }
 
-/* Enqueue the kernels of the plan on the workspace stream. */
-static int enqueue_steps(const pyc_ir_module* m, const hip_plan* plan, char* why, size_t why_cap) {
+/* Enqueue the kernels of the plan on the workspace stream; vp[v] is the
+ * device storage of value v (workspace, or the caller's device tensor). */
+static int enqueue_steps(const pyc_ir_module* m, const hip_plan* plan, void* const* vp, char* why, size_t why_cap) {
     size_t s;
     void* st_stream = (void*)g_ws.stream;
     for (s = 0; s < plan->nsteps; ++s) {
         const hip_step* st = &plan->steps[s];
-        void* out = g_ws.val[st->out].ptr;
+        void* out = vp[st->out];
         const size_t clen = w8_chain_len(plan, s);
         if (clen >= 2) {
             /* the whole run of fp8-weight steps in one launch */
@@ -780,14 +824,14 @@ static int enqueue_steps(const pyc_ir_module* m, const hip_plan* plan, char* why
             size_t c;
             for (c = 0; c < clen; ++c) {
                 const hip_step* q = &plan->steps[s + c];
-                wq[c] = g_ws.val[q->in[1]].ptr;
-                sc[c] = (const float*)g_ws.val[q->in[2]].ptr;
+                wq[c] = vp[q->in[1]];
+                sc[c] = (const float*)vp[q->in[2]];
                 cn[c] = q->n;
                 ck[c] = q->k;
                 cr[c] = q->relu;
             }
-            if (pyc_hip_w8a16_chain_dispatch("hip_w8a16_chain_e4m3", st->m, (int)clen, g_ws.val[st->in[0]].ptr, wq,
-                                             sc, cn, ck, cr, g_ws.val[plan->steps[s + clen - 1].out].ptr,
+            if (pyc_hip_w8a16_chain_dispatch("hip_w8a16_chain_e4m3", st->m, (int)clen, vp[st->in[0]], wq,
+                                             sc, cn, ck, cr, vp[plan->steps[s + clen - 1].out],
                                              st_stream) != 0) {
                 snprintf(why, why_cap, "hip_kernel_failed:hip_w8a16_chain_e4m3");
                 return -1;
@@ -804,11 +848,11 @@ static int enqueue_steps(const pyc_ir_module* m, const hip_plan* plan, char* why
             /* an fp32 row bias is read where it was uploaded; scalar and half
              * operands use their converted fp32 copy */
             bias = (st->add_mode == ADD_ROW_BIAS && !plan->f32_bias_needed[st->add_in])
-                       ? (const float*)g_ws.val[st->add_in].ptr
+                       ? (const float*)vp[st->add_in]
                        : (const float*)g_ws.bias32[st->add_in].ptr;
         } else if (st->add_mode == ADD_MATRIX) {
             /* C starts as the addend; beta = 1 folds it into the epilogue */
-            if (hipMemcpyAsync(out, g_ws.val[st->add_in].ptr, (size_t)st->m * st->n * dtype_bytes(st->dtype),
+            if (hipMemcpyAsync(out, vp[st->add_in], (size_t)st->m * st->n * dtype_bytes(st->dtype),
                                hipMemcpyDeviceToDevice, g_ws.stream) != hipSuccess) {
                 snprintf(why, why_cap, "hip_copy_failed");
                 return -1;
@@ -817,25 +861,25 @@ static int enqueue_steps(const pyc_ir_module* m, const hip_plan* plan, char* why
         }
         switch (st->kind) {
             case ST_GEMM:
-                rc = pyc_hip_gemm_dispatch(st->symbol, st->m, st->n, st->k, g_ws.val[st->in[0]].ptr,
-                                           g_ws.val[st->in[1]].ptr, out, 1.0f, beta, bias, epi, st_stream);
+                rc = pyc_hip_gemm_dispatch(st->symbol, st->m, st->n, st->k, vp[st->in[0]],
+                                           vp[st->in[1]], out, 1.0f, beta, bias, epi, st_stream);
                 break;
             case ST_W8A16:
-                rc = pyc_hip_w8a16_gemm_dispatch(st->symbol, st->m, st->n, st->k, g_ws.val[st->in[0]].ptr,
-                                                 g_ws.val[st->in[1]].ptr, (const float*)g_ws.val[st->in[2]].ptr,
+                rc = pyc_hip_w8a16_gemm_dispatch(st->symbol, st->m, st->n, st->k, vp[st->in[0]],
+                                                 vp[st->in[1]], (const float*)vp[st->in[2]],
                                                  st->relu, out, st_stream);
                 break;
             case ST_CONV:
                 rc = pyc_hip_conv2d_dispatch(st->symbol, st->conv[0], st->conv[1], st->conv[2], st->conv[3],
                                              st->conv[4], st->conv[5], st->conv[6], st->conv[7], st->conv[8],
-                                             st->conv[9], st->conv[10], g_ws.val[st->in[0]].ptr,
-                                             g_ws.val[st->in[1]].ptr, bias, st->relu, out, st_stream);
+                                             st->conv[9], st->conv[10], vp[st->in[0]],
+                                             vp[st->in[1]], bias, st->relu, out, st_stream);
                 break;
             case ST_ATTN: {
                 const float scale = 1.0f / sqrtf((float)st->attn[3]);
                 rc = pyc_hip_attention_dispatch(st->symbol, st->attn[0], st->attn[1], st->attn[2], st->attn[3],
-                                                st->attn[4], g_ws.val[st->in[0]].ptr, g_ws.val[st->in[1]].ptr,
-                                                g_ws.val[st->in[2]].ptr, out, scale, st_stream);
+                                                st->attn[4], vp[st->in[0]], vp[st->in[1]],
+                                                vp[st->in[2]], out, scale, st_stream);
                 break;
             }
             default:
@@ -859,6 +903,11 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
     const int skip_out = env_true("PYC_CUDA_SKIP_HOST_OUTPUT_COPY");
     const int use_graph = env_default_true("PYC_CUDA_ENABLE_GRAPH_REPLAY");
     int copy_in[PYC_IR_MAX_OPS];
+    void* vp[PYC_IR_MAX_OPS];   /* device storage of each value: workspace or the caller's device tensor */
+    int dev_in[PYC_IR_MAX_OPS]; /* INPUT op bound to the caller's device tensor (no staging, no copy) */
+    int dev_out[64];            /* output whose caller tensor is device memory */
+    int out_d2d[64];            /* ... filled by a device-to-device copy (its value is stored elsewhere) */
+    int any_dev = 0;
     size_t i;
     uint64_t sig = 1469598103934665603ull;
     int replayed = 0;
@@ -878,15 +927,21 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
     }
 
     /* bind inputs, size checks, device + staging buffers */
+    memset(vp, 0, sizeof(vp));
+    memset(dev_in, 0, sizeof(dev_in));
+    memset(dev_out, 0, sizeof(dev_out));
+    memset(out_d2d, 0, sizeof(out_d2d));
     for (i = 0; i < m->op_count; ++i) {
         const int ord = plan.input_ordinal[i];
         size_t bytes;
+        copy_in[i] = 0;
         if (ord < 0) {
             if (plan.value_bytes[i] && plan.value_op[i] == (int)i &&
                 dgrow(&g_ws.val[i], plan.value_bytes[i]) != 0) {
                 snprintf(why, why_cap, "hip_malloc_failed");
                 return -1;
             }
+            vp[i] = g_ws.val[i].ptr;
             continue;
         }
         if ((size_t)ord >= input_count || !inputs[ord].data) {
@@ -896,10 +951,16 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
         if (inputs[ord].dtype != m->ops[i].dtype || inputs[ord].size_bytes < bytes) {
             return 1;
         }
+        if (is_device_ptr(inputs[ord].data)) {
+            dev_in[i] = 1; /* read in place */
+            vp[i] = inputs[ord].data;
+            continue;
+        }
         if (dgrow(&g_ws.val[i], bytes) != 0 || hgrow(&g_ws.stage_in[i], bytes) != 0) {
             snprintf(why, why_cap, "hip_malloc_failed");
             return -1;
         }
+        vp[i] = g_ws.val[i].ptr;
         copy_in[i] = 1;
         if (g_ws.uploaded[i] && g_ws.last_host[i] == inputs[ord].data && g_ws.last_bytes[i] == bytes &&
             ((plan.is_weight[i] && static_rhs) || (!plan.is_weight[i] && static_lhs))) {
@@ -909,11 +970,28 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
     for (i = 0; i < plan.n_outputs; ++i) {
         const int src = plan.output_src[i];
         const size_t bytes = plan.value_bytes[src];
-        if (!skip_out && (!outputs[i].data || outputs[i].size_bytes < bytes)) {
-            return 1;
-        }
         if (outputs[i].dtype != plan.vdtype[src]) {
             return 1; /* output dtype must match the produced value */
+        }
+        if (outputs[i].data && is_device_ptr(outputs[i].data)) {
+            size_t j;
+            int bound = plan.input_ordinal[src] >= 0; /* an input passed through: copy it */
+            if (outputs[i].size_bytes < bytes) {
+                return 1;
+            }
+            for (j = 0; j < i; ++j) {
+                bound |= dev_out[j] && !out_d2d[j] && plan.output_src[j] == src; /* value already written elsewhere */
+            }
+            dev_out[i] = 1;
+            if (bound) {
+                out_d2d[i] = 1;
+            } else {
+                vp[src] = outputs[i].data; /* the producing step writes the caller's tensor */
+            }
+            continue;
+        }
+        if (!skip_out && (!outputs[i].data || outputs[i].size_bytes < bytes)) {
+            return 1;
         }
         if (hgrow(&g_ws.stage_out[i], bytes) != 0) {
             snprintf(why, why_cap, "hip_malloc_failed");
@@ -937,23 +1015,39 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
                 return 1;
             }
             {
-                /* small host-side conversion / broadcast, then one upload */
+                /* small host-side conversion / broadcast, then one upload (an
+                 * operand in device memory is first read back: it is a [N] or
+                 * [1] vector) */
                 float* tmp = (float*)malloc(cols * sizeof(float));
+                const void* hsrc = inputs[ord].data;
+                void* hcopy = NULL;
                 size_t c;
                 if (!tmp) {
                     return -1;
+                }
+                if (dev_in[st->add_in]) {
+                    const size_t nb = (st->add_mode == ADD_SCALAR ? 1 : cols) * dtype_bytes(m->ops[st->add_in].dtype);
+                    hcopy = malloc(nb);
+                    if (!hcopy || hipMemcpy(hcopy, inputs[ord].data, nb, hipMemcpyDeviceToHost) != hipSuccess) {
+                        free(hcopy);
+                        free(tmp);
+                        snprintf(why, why_cap, "hip_copy_failed");
+                        return -1;
+                    }
+                    hsrc = hcopy;
                 }
                 for (c = 0; c < cols; ++c) {
                     const size_t src_i = st->add_mode == ADD_SCALAR ? 0 : c;
                     const pyc_dtype dt = m->ops[st->add_in].dtype;
                     if (dt == PYC_DTYPE_F32) {
-                        tmp[c] = ((const float*)inputs[ord].data)[src_i];
+                        tmp[c] = ((const float*)hsrc)[src_i];
                     } else if (dt == PYC_DTYPE_BF16) {
-                        tmp[c] = bf16_bits_to_f32(((const uint16_t*)inputs[ord].data)[src_i]);
+                        tmp[c] = bf16_bits_to_f32(((const uint16_t*)hsrc)[src_i]);
                     } else {
-                        tmp[c] = f16_bits_to_f32(((const uint16_t*)inputs[ord].data)[src_i]);
+                        tmp[c] = f16_bits_to_f32(((const uint16_t*)hsrc)[src_i]);
                     }
                 }
+                free(hcopy);
                 if (hipMemcpy(g_ws.bias32[st->add_in].ptr, tmp, cols * sizeof(float), hipMemcpyHostToDevice) != hipSuccess) {
                     free(tmp);
                     snprintf(why, why_cap, "hip_copy_failed");
@@ -971,6 +1065,21 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
     for (i = 0; i < m->op_count; ++i) {
         if (plan.input_ordinal[i] >= 0) {
             sig = fnv(sig, &copy_in[i], sizeof(int));
+            sig = fnv(sig, &dev_in[i], sizeof(int));
+        }
+    }
+    for (i = 0; i < m->op_count; ++i) {
+        any_dev |= dev_in[i];
+    }
+    for (i = 0; i < plan.n_outputs; ++i) {
+        any_dev |= dev_out[i];
+    }
+    /* a graph bakes in the caller's device tensors: their addresses are part of the run */
+    sig = fnv(sig, vp, sizeof(vp));
+    for (i = 0; i < plan.n_outputs; ++i) {
+        sig = fnv(sig, &dev_out[i], sizeof(int));
+        if (dev_out[i]) {
+            sig = fnv(sig, &outputs[i].data, sizeof(void*));
         }
     }
 
@@ -1029,15 +1138,20 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
                 rc = hipEventRecord(g_ws.ev0, g_ws.stream) == hipSuccess ? 0 : -1;
             }
             if (rc == 0) {
-                rc = enqueue_steps(m, &plan, why, why_cap);
+                rc = enqueue_steps(m, &plan, vp, why, why_cap);
             }
             if (rc == 0 && !use_graph) {
                 rc = hipEventRecord(g_ws.ev1, g_ws.stream) == hipSuccess ? 0 : -1;
             }
-            for (i = 0; rc == 0 && !skip_out && i < plan.n_outputs; ++i) {
+            for (i = 0; rc == 0 && i < plan.n_outputs; ++i) {
                 const int src = plan.output_src[i];
-                if (hipMemcpyAsync(g_ws.stage_out[i].ptr, g_ws.val[src].ptr, plan.value_bytes[src],
-                                   hipMemcpyDeviceToHost, g_ws.stream) != hipSuccess) {
+                if (dev_out[i]) {
+                    if (out_d2d[i] && hipMemcpyAsync(outputs[i].data, vp[src], plan.value_bytes[src],
+                                                     hipMemcpyDeviceToDevice, g_ws.stream) != hipSuccess) {
+                        rc = -1;
+                    }
+                } else if (!skip_out && hipMemcpyAsync(g_ws.stage_out[i].ptr, vp[src], plan.value_bytes[src],
+                                                       hipMemcpyDeviceToHost, g_ws.stream) != hipSuccess) {
                     rc = -1;
                 }
             }
@@ -1071,6 +1185,14 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
     }
 
     t0 = now_ms();
+    if (any_dev) {
+        /* the caller's device tensors may come from work on any stream: the
+         * backend's own stream does not order against those, so wait for it */
+        if (hipDeviceSynchronize() != hipSuccess) {
+            snprintf(why, why_cap, "hip_sync_failed");
+            return -1;
+        }
+    }
     if (use_graph) {
         if (hipEventRecord(g_ws.ev0, g_ws.stream) != hipSuccess ||
             hipGraphLaunch(g_ws.gexec, g_ws.stream) != hipSuccess ||
@@ -1094,7 +1216,9 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
     /* pinned staging -> caller buffers */
     t0 = now_ms();
     for (i = 0; !skip_out && i < plan.n_outputs; ++i) {
-        memcpy(outputs[i].data, g_ws.stage_out[i].ptr, plan.value_bytes[plan.output_src[i]]);
+        if (!dev_out[i]) {
+            memcpy(outputs[i].data, g_ws.stage_out[i].ptr, plan.value_bytes[plan.output_src[i]]);
+        }
     }
     if (trace) {
         trace->copy_out_ms += now_ms() - t0;
@@ -1303,6 +1427,7 @@ static pyc_cuda_dispatch_status dispatch_locked(const pyc_ir_module* module, con
     int available;
     int supported;
     int native_rc = 1;
+    int dev_tensors = 0;
 
     if (!module || !inputs || !outputs || !cpu_executor) {
         return PYC_CUDA_DISPATCH_ERROR;
@@ -1326,6 +1451,10 @@ static pyc_cuda_dispatch_status dispatch_locked(const pyc_ir_module* module, con
         trace->cuda_available = available;
     }
     supported = native_kind_supported(module);
+    /* Tensors in device memory (an extension: the reference takes host
+     * pointers only) can be run only natively; the simulated and CPU
+     * executors read host memory. */
+    dev_tensors = available && any_device_tensor(inputs, input_count, outputs, output_count);
     if (available && supported && !env_true("PYC_CUDA_FORCE_FALLBACK")) {
         int count = 0;
         /* a real device is tried first, also when the simulation flag is set
@@ -1344,7 +1473,7 @@ static pyc_cuda_dispatch_status dispatch_locked(const pyc_ir_module* module, con
                 ws_release();
             }
         }
-        if (env_true("PYC_CUDA_SIMULATE_AVAILABLE") &&
+        if (!dev_tensors && env_true("PYC_CUDA_SIMULATE_AVAILABLE") &&
             execute_simulated(module, inputs, input_count, outputs, output_count) == 0) {
             if (trace) {
                 trace->fallback_to_cpu = 0;
@@ -1354,6 +1483,17 @@ static pyc_cuda_dispatch_status dispatch_locked(const pyc_ir_module* module, con
         }
     }
 
+    if (dev_tensors) {
+        if (trace) {
+            trace->fallback_to_cpu = 0;
+            if (native[0] != '\0') {
+                snprintf(trace->reason, sizeof(trace->reason), "%.90s;device_tensors_no_cpu_fallback", native);
+            } else {
+                set_reason(trace->reason, sizeof(trace->reason), "device_tensors_no_cpu_fallback");
+            }
+        }
+        return PYC_CUDA_DISPATCH_ERROR;
+    }
     if (cpu_executor(module, inputs, input_count, outputs, output_count, executor_ctx) != 0) {
         if (trace) {
             trace->fallback_to_cpu = 0;

@@ -1,0 +1,205 @@
+"""GPU: pyc_run_model with tensors that live in device memory (the device-
+resident tensors of the reference survey's first "next" item). The backend
+binds such tensors to the plan directly (no staging, no host copies) and
+includes their addresses in the graph signature; host and device tensors may
+be mixed. Every run here is checked bit for bit against the same module run
+with host buffers (the same kernels on the same values), and the host runs
+are themselves checked against the oracle in tests/test_gpu_engine.py."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle
+from pyc_amd import abi
+from tests import engine_util as eu
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True)
+def _strict(monkeypatch, gpu):
+    for k in ("PYC_CUDA_SIMULATE_AVAILABLE", "PYC_CUDA_DISABLE", "PYC_CUDA_FORCE_FALLBACK", "PYC_CUDA_FORCE_ERROR",
+              "PYC_CUDA_SKIP_HOST_OUTPUT_COPY", "PYC_CUDA_ASSUME_STATIC_LHS", "PYC_CUDA_ASSUME_STATIC_RHS"):
+        monkeypatch.delenv(k, raising=False)
+    monkeypatch.setenv("PYC_HIP_STRICT", "1")
+
+
+def _dt(t, dtype):
+    """pyc_tensor describing a torch device tensor."""
+    x = abi.Tensor()
+    x.data = t.data_ptr()
+    x.size_bytes = t.numel() * t.element_size()
+    x.dtype = dtype
+    x.shape = abi.make_shape(tuple(t.shape))
+    return x
+
+
+def _ht(a, dtype):
+    return eu.tensor(a, dtype)
+
+
+def _run(mdl, ins, outs):
+    I = (abi.Tensor * len(ins))(*ins)
+    O = (abi.Tensor * len(outs))(*outs)
+    st = abi.RunStats()
+    rc = mdl.L.pyc_run_model(mdl.h, I, len(ins), O, len(outs), C.byref(st))
+    return rc, st
+
+
+def _gemm_module(M, K, N, dtype=abi.DTYPE_F32, bias_dtype=None):
+    bias_dtype = dtype if bias_dtype is None else bias_dtype
+    ops = [eu.op(abi.OP_INPUT, "x", (M, K), dtype=dtype), eu.op(abi.OP_INPUT, "w", (K, N), dtype=dtype),
+           eu.op(abi.OP_INPUT, "bias", (N,), dtype=bias_dtype), eu.op(abi.OP_MATMUL, "matmul0", (), (0, 1), dtype=dtype),
+           eu.op(abi.OP_ADD, "add0", (), (3, 2), dtype=dtype), eu.op(abi.OP_RELU, "relu0", (), (4,), dtype=dtype),
+           eu.op(abi.OP_OUTPUT, "out0", (M, N), (5,), dtype=dtype)]
+    return eu.Model(eu.mine(), ops, backend=abi.BACKEND_CUDA)
+
+
+def test_device_tensors_f32_gemm_bias_relu(gpu):
+    """Config 1's module shape (smaller): every tensor on the device; equal to
+    the host-buffer run; no copy time; graph replay on the second call."""
+    torch = gpu
+    M, K, N = 512, 384, 256
+    r = np.random.default_rng(0)
+    x, w = (r.uniform(-1, 1, s).astype(np.float32) for s in ((M, K), (K, N)))
+    b = r.uniform(-1, 1, N).astype(np.float32)
+    mdl = _gemm_module(M, K, N)
+    assert mdl.status == 0
+    st, (host_out,), s = mdl.run([x, w, b], [(M, N)])
+    assert st == 0 and s.execution_path.decode().startswith("hip_native")
+    X, W, Bv = (torch.from_numpy(t).cuda() for t in (x, w, b))
+    Y = torch.full((M, N), float("nan"), device="cuda")
+    torch.cuda.synchronize()
+    paths = []
+    for _ in range(2):
+        rc, s = _run(mdl, [_dt(X, abi.DTYPE_F32), _dt(W, abi.DTYPE_F32), _dt(Bv, abi.DTYPE_F32)],
+                     [_dt(Y, abi.DTYPE_F32)])
+        assert rc == 0, s.execution_path
+        paths.append(s.execution_path.decode())
+        assert np.array_equal(Y.cpu().numpy(), host_out)
+        assert s.cuda_copy_in_ms < 0.5 and s.cuda_copy_out_ms < 0.5
+    mdl.close()
+    assert paths[0].startswith("hip_native_graph_capture") and paths[1].startswith("hip_native_graph_replay"), paths
+
+
+def test_device_tensors_rebind_and_mixed(gpu):
+    """New device addresses re-capture the graph (the old one baked in the old
+    ones); host and device tensors in one call; a host run after device runs."""
+    torch = gpu
+    M, K, N = 256, 128, 192
+    r = np.random.default_rng(1)
+    mdl = _gemm_module(M, K, N)
+    cases = []
+    for seed in range(3):
+        x, w = (r.uniform(-1, 1, s).astype(np.float32) for s in ((M, K), (K, N)))
+        b = r.uniform(-1, 1, N).astype(np.float32)
+        st, (ref,), _ = mdl.run([x, w, b], [(M, N)])
+        assert st == 0
+        cases.append((x, w, b, ref.copy()))
+    outs = [torch.empty((M, N), device="cuda") for _ in range(2)]
+    for i, (x, w, b, ref) in enumerate(cases):
+        X, W = torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda()
+        Y = outs[i % 2]
+        torch.cuda.synchronize()
+        # x on the device, w on the device, bias from host memory, output on the device
+        rc, s = _run(mdl, [_dt(X, abi.DTYPE_F32), _dt(W, abi.DTYPE_F32), _ht(b, abi.DTYPE_F32)], [_dt(Y, abi.DTYPE_F32)])
+        assert rc == 0, s.execution_path
+        assert "graph_capture" in s.execution_path.decode()  # new input addresses every time
+        assert np.array_equal(Y.cpu().numpy(), ref), f"case {i}"
+        # host output from the same device inputs
+        host_y = np.zeros((M, N), np.float32)
+        rc, s = _run(mdl, [_dt(X, abi.DTYPE_F32), _dt(W, abi.DTYPE_F32), _ht(b, abi.DTYPE_F32)],
+                     [_ht(host_y, abi.DTYPE_F32)])
+        assert rc == 0 and np.array_equal(host_y, ref), f"case {i} host output"
+    x, w, b, ref = cases[0]
+    st, (out,), _ = mdl.run([x, w, b], [(M, N)])
+    assert st == 0 and np.array_equal(out, ref)
+    mdl.close()
+
+
+def test_device_tensors_bf16_half_bias(gpu):
+    """A bf16 GEMM whose bias is a bf16 device vector: the backend reads it back
+    for its fp32 copy (the host path converts it in host memory)."""
+    torch = gpu
+    M, K, N = 256, 512, 384
+    r = np.random.default_rng(2)
+    a = oracle.f32_to_bf16((r.standard_normal((M, K)) / 16).astype(np.float32))
+    w = oracle.f32_to_bf16(r.standard_normal((K, N)).astype(np.float32))
+    b = oracle.f32_to_bf16(r.standard_normal(N).astype(np.float32))
+    mdl = _gemm_module(M, K, N, dtype=abi.DTYPE_BF16)
+    assert mdl.status == 0
+    st, (ref,), s = mdl.run([a, w, b], [(M, N)], in_dtypes=[abi.DTYPE_BF16] * 3, out_dtypes=[abi.DTYPE_BF16],
+                            out_np_dtype=np.uint16)
+    assert st == 0, s.execution_path
+    A, Wd, Bd = (torch.from_numpy(t.view(np.int16)).cuda() for t in (a, w, b))
+    Y = torch.zeros((M, N), dtype=torch.int16, device="cuda")
+    torch.cuda.synchronize()
+    rc, s = _run(mdl, [_dt(A, abi.DTYPE_BF16), _dt(Wd, abi.DTYPE_BF16), _dt(Bd, abi.DTYPE_BF16)],
+                 [_dt(Y, abi.DTYPE_BF16)])
+    mdl.close()
+    assert rc == 0, s.execution_path
+    assert np.array_equal(Y.cpu().numpy().view(np.uint16), ref)
+
+
+def test_device_tensors_decode_chain(gpu):
+    """The fp8 decode-chain module (one chain launch) with all weights, scales,
+    activations and the output on the device."""
+    torch = gpu
+    M, D, F = 32, 256, 512
+    r = np.random.default_rng(3)
+    x = oracle.f32_to_bf16(r.standard_normal((M, D)).astype(np.float32))
+    ops, ins, dts = [eu.op(abi.OP_INPUT, "x", (M, D), dtype=abi.DTYPE_BF16)], [x], [abi.DTYPE_BF16]
+    cur = 0
+    for l in range(2):
+        wu, su = oracle.quantize_e4m3_per_col((r.standard_normal((D, F)) * np.sqrt(2 / D)).astype(np.float32))
+        wd, sd = oracle.quantize_e4m3_per_col((r.standard_normal((F, D)) * np.sqrt(2 / F)).astype(np.float32))
+        base = len(ops)
+        ops += [eu.op(abi.OP_INPUT, f"wu{l}", (F, D), dtype=abi.DTYPE_FP8_E4M3), eu.op(abi.OP_INPUT, f"su{l}", (F,)),
+                eu.op(abi.OP_INPUT, f"wd{l}", (D, F), dtype=abi.DTYPE_FP8_E4M3), eu.op(abi.OP_INPUT, f"sd{l}", (D,))]
+        ins += [wu, su, wd, sd]
+        dts += [abi.DTYPE_FP8_E4M3, abi.DTYPE_F32, abi.DTYPE_FP8_E4M3, abi.DTYPE_F32]
+        ops += [eu.op(abi.OP_MATMUL, f"up{l}", (), (cur, base, base + 1), dtype=abi.DTYPE_BF16),
+                eu.op(abi.OP_RELU, f"relu{l}", (), (base + 4,), dtype=abi.DTYPE_BF16),
+                eu.op(abi.OP_MATMUL, f"down{l}", (), (base + 5, base + 2, base + 3), dtype=abi.DTYPE_BF16)]
+        cur = base + 6
+    ops.append(eu.op(abi.OP_OUTPUT, "y", (M, D), (cur,), dtype=abi.DTYPE_BF16))
+    mdl = eu.Model(eu.mine(), ops, backend=abi.BACKEND_CUDA)
+    assert mdl.status == 0
+    st, (ref,), s = mdl.run(ins, [(M, D)], in_dtypes=dts, out_dtypes=[abi.DTYPE_BF16], out_np_dtype=np.uint16)
+    assert st == 0 and "hip_w8a16_chain_e4m3" in s.execution_path.decode()
+    dev = [torch.from_numpy(np.ascontiguousarray(a).view(np.uint8)).cuda() for a in ins]
+    Y = torch.zeros((M, D), dtype=torch.int16, device="cuda")
+    torch.cuda.synchronize()
+    tens = []
+    for t, a, d in zip(dev, ins, dts):
+        x_ = _dt(t, d)
+        x_.shape = abi.make_shape(a.shape)
+        tens.append(x_)
+    rc, s = _run(mdl, tens, [_dt(Y, abi.DTYPE_BF16)])
+    mdl.close()
+    assert rc == 0, s.execution_path
+    assert "hip_w8a16_chain_e4m3" in s.execution_path.decode()
+    assert np.array_equal(Y.cpu().numpy().view(np.uint16), ref)
+
+
+def test_device_tensors_never_reach_cpu_executor(gpu, monkeypatch):
+    """A forced CPU fallback with device tensors is an error (the CPU executor
+    reads host memory), not a run of the CPU executor on device addresses."""
+    torch = gpu
+    monkeypatch.delenv("PYC_HIP_STRICT", raising=False)
+    monkeypatch.setenv("PYC_CUDA_FORCE_FALLBACK", "1")
+    M, K, N = 64, 64, 64
+    mdl = _gemm_module(M, K, N)
+    X, W = torch.rand((M, K), device="cuda"), torch.rand((K, N), device="cuda")
+    Bv, Y = torch.rand(N, device="cuda"), torch.empty((M, N), device="cuda")
+    torch.cuda.synchronize()
+    rc, s = _run(mdl, [_dt(X, abi.DTYPE_F32), _dt(W, abi.DTYPE_F32), _dt(Bv, abi.DTYPE_F32)], [_dt(Y, abi.DTYPE_F32)])
+    assert rc == abi.STATUS_RUNTIME_FAILED, rc
+    assert "device_tensors_no_cpu_fallback" in s.execution_path.decode(), s.execution_path
+    # the same module with host buffers still falls back as the reference does
+    x = np.ones((M, K), np.float32)
+    st, (out,), s = mdl.run([x, np.ones((K, N), np.float32), np.zeros(N, np.float32)], [(M, N)])
+    mdl.close()
+    assert st == 0 and s.fallback_count >= 1
+    assert np.allclose(out, K)
