@@ -622,7 +622,7 @@ __global__ void __launch_bounds__(kCWaves * kWave, 1) w8a16_chain_kernel(W8Chain
     // weight / X part of item (unit, kk) of a step, from that step's descriptors
     auto dma_w = [&](const i32x4& wrs, int K, int unit, int kk, int stage) {
         const uint32_t wvo = (uint32_t)(unit * kW8Rows + wrow) * (uint32_t)K + wcol;
-        lds_dma_buf_b128_u(wrs, wvo, (uint32_t)(kk * kQK), wlds + (uint32_t)stage * kQStageBytes);
+        lds_dma_buf_b128_nt_u(wrs, wvo, (uint32_t)(kk * kQK), wlds + (uint32_t)stage * kQStageBytes);
     };
     auto dma_x = [&](const i32x4& xrs, uint32_t xvo, int kk, int stage) {
         lds_dma_buf_b128_u(xrs, xvo, (uint32_t)(kk * kQK * 2), xlds + (uint32_t)stage * kQStageBytes);

@@ -31,6 +31,19 @@ __device__ inline void lds_dma_buf_b128_u(i32x4 rsrc, uint32_t voff, uint32_t so
     lds_dma_buf_b128(r, voff, __builtin_amdgcn_readfirstlane(soff), __builtin_amdgcn_readfirstlane(lds_base));
 }
 
+// Same, with the non-temporal (streaming) cache policy: for data read once
+// per launch and larger than the caches (the decode chain's weights), so it
+// does not evict what is reread soon (the chain's activations and partials).
+__device__ inline void lds_dma_buf_b128_nt_u(i32x4 rsrc, uint32_t voff, uint32_t soff, uint32_t lds_base) {
+    const i32x4 r = i32x4{__builtin_amdgcn_readfirstlane(rsrc.x), __builtin_amdgcn_readfirstlane(rsrc.y),
+                          __builtin_amdgcn_readfirstlane(rsrc.z), __builtin_amdgcn_readfirstlane(rsrc.w)};
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen nt lds"
+                 :
+                 : "s"(__builtin_amdgcn_readfirstlane(lds_base)), "v"(voff), "s"(r),
+                   "s"(__builtin_amdgcn_readfirstlane(soff))
+                 : "memory", "m0");
+}
+
 // Raw buffer descriptor (CDNA layout): 48-bit base, stride 0, byte count,
 // 32-bit data format. Every field is wave-uniform.
 __device__ inline i32x4 make_buf_rsrc(const void* base, uint32_t bytes) {

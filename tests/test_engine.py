@@ -520,3 +520,40 @@ def test_unsupported_kind_reason(monkeypatch):
     # GELU has no lowering anywhere: the CPU executor refuses it too
     assert st == abi.STATUS_RUNTIME_FAILED and lf["cuda_reason"] == "cpu_fallback_failed"
     assert s.graph_break_gelu_count == 1
+
+
+def test_engine_wrapper_cpu_backend():
+    """pyc_amd.engine (the Python side of the run path that bench.py's engine
+    workload uses) on the CPU backend: matmul+bias+ReLU through
+    pyc_compile_model/pyc_run_model equals the oracle's CPU executor result bit
+    for bit, and run_stats_json carries the reference bench driver's fields."""
+    import oracle
+    from pyc_amd import abi, engine
+
+    M, K, N = 16, 24, 8
+    r = np.random.default_rng(3)
+    x, w = r.uniform(-1, 1, (M, K)).astype(np.float32), r.uniform(-1, 1, (K, N)).astype(np.float32)
+    b = r.uniform(-1, 1, N).astype(np.float32)
+    ops = [engine.op(abi.OP_INPUT, "x", (M, K)), engine.op(abi.OP_INPUT, "w", (K, N)),
+           engine.op(abi.OP_INPUT, "bias", (N,)), engine.op(abi.OP_MATMUL, "matmul0", (), (0, 1)),
+           engine.op(abi.OP_ADD, "add0", (), (3, 2)), engine.op(abi.OP_RELU, "relu0", (), (4,)),
+           engine.op(abi.OP_OUTPUT, "out0", (M, N), (5,))]
+    model = engine.Model(ops, backend=abi.BACKEND_CPU)
+    assert model.status == 0
+    y = np.zeros((M, N), np.float32)
+    stats, wall = [], []
+    for _ in range(3):
+        rc, st = model.run([engine.host_tensor(a, abi.DTYPE_F32) for a in (x, w, b)],
+                           [engine.host_tensor(y, abi.DTYPE_F32)])
+        assert rc == 0
+        stats.append(st)
+        wall.append(st.run_ms)
+    ref = np.maximum(oracle.matmul_f32(x, w) + b[None, :], 0.0)
+    assert np.array_equal(y, ref.astype(np.float32))
+    j = engine.run_stats_json(stats, wall, model)
+    model.close()
+    for key in ("latency_ms", "peak_memory_bytes", "profile", "controller", "execution_path", "kernel_selection",
+                "compile_options", "reliability", "phantom_graph", "precision_policy"):
+        assert key in j, key
+    assert set(j["latency_ms"]) == {"mean", "p50", "p95", "min", "max"}
+    assert j["execution_path"].startswith("cpu"), j["execution_path"]
