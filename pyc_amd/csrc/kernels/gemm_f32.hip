@@ -9,7 +9,7 @@
 // the row-bias + ReLU epilogue the reference ran on the host after the copy
 // back (reference cuda_backend.c:1697-1742).
 //
-// Tile 64x64x32, 4 waves (2x2) of 32x32; each lane reads 4 consecutive k of
+// Tile 64x64x64, 4 waves (2x2) of 32x32; each lane reads 4 consecutive k of
 // its row as one 16-byte LDS load and issues 4 MFMAs, one per element, so A
 // and B use the same k permutation {4*(lane/16)+e}. B is staged in LDS as
 // [n][k] for both layouts ([K,N] tiles are transposed on the LDS store).
@@ -19,8 +19,11 @@ namespace pyc {
 
 constexpr int kF32BM = 64;
 constexpr int kF32BN = 64;
-constexpr int kF32BK = 32;
-constexpr int kF32Ch = kF32BK / 4;  // 16-byte chunks per LDS row (8)
+// K depth 64: one tile's MFMAs (about 1 us at 1024^3, one workgroup per CU)
+// cover the global loads of the next tile, which depth 32 did not
+constexpr int kF32BK = 64;
+constexpr int kF32Ch = kF32BK / 4;  // 16-byte chunks per LDS row (16)
+constexpr int kF32Ld = kF32BM * kF32Ch / 256;  // 16-byte loads per thread per operand tile (4)
 
 __device__ inline int swz8(int row, int chunk) { return chunk ^ (row & 7); }
 
@@ -42,8 +45,8 @@ gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ B, float*
     const bool vec_k = (K & 3) == 0;
     const bool vec_n = (N & 3) == 0;
 
-    // 64 rows x 8 chunks = 512 chunks per operand tile -> 2 per thread.
-    f32x4 ra[2], rb[2];
+    // 64 rows x 16 chunks = 1024 chunks per operand tile -> 4 per thread.
+    f32x4 ra[kF32Ld], rb[kF32Ld];
 
     auto ld4 = [&](const float* base, int r, int rmax, int c, int cmax, bool vec, size_t ld) -> f32x4 {
         if (!GUARD) return *reinterpret_cast<const f32x4*>(base + (size_t)r * ld + c);
@@ -55,34 +58,37 @@ gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ B, float*
     };
     auto load = [&](int k0) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < kF32Ld; ++i) {
             const int q = tid + i * 256;
-            const int row = q >> 3, ch = q & 7;
+            const int row = q / kF32Ch, ch = q % kF32Ch;
             ra[i] = ld4(A, m0 + row, M, k0 + ch * 4, K, vec_k, (size_t)K);
             if (BT) {
                 rb[i] = ld4(B, n0 + row, N, k0 + ch * 4, K, vec_k, (size_t)K);
             } else {
-                // [K,N] tile: 32 k rows x 16 chunks of 4 columns.
-                const int kr = q >> 4, nc = q & 15;
-                rb[i] = ld4(B, k0 + kr, K, n0 + nc * 4, N, vec_n, (size_t)N);
+                // [K,N] tile: thread tid holds the 4 x 4 block of k rows
+                // 4*(tid/16) + i and columns 4*(tid%16) .. +3 (16 threads
+                // read one whole 256-byte row segment)
+                rb[i] = ld4(B, k0 + 4 * (tid >> 4) + i, K, n0 + 4 * (tid & 15), N, vec_n, (size_t)N);
             }
         }
     };
     auto store = [&](int buf) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < kF32Ld; ++i) {
             const int q = tid + i * 256;
-            const int row = q >> 3, ch = q & 7;
+            const int row = q / kF32Ch, ch = q % kF32Ch;
             *reinterpret_cast<f32x4*>(&As[buf][row * kF32BK + swz8(row, ch) * 4]) = ra[i];
-            if (BT) {
-                *reinterpret_cast<f32x4*>(&Bs[buf][row * kF32BK + swz8(row, ch) * 4]) = rb[i];
-            } else {
-                const int kr = q >> 4, nc = q & 15;
+            if (BT) *reinterpret_cast<f32x4*>(&Bs[buf][row * kF32BK + swz8(row, ch) * 4]) = rb[i];
+        }
+        if (!BT) {
+            // the 4 x 4 block transposed in registers: column j of it is the
+            // 16-byte chunk tid/16 (k = 4*(tid/16) .. +3) of LDS row n
+            const int kc = tid >> 4;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int n = nc * 4 + j;
-                    Bs[buf][n * kF32BK + swz8(n, kr >> 2) * 4 + (kr & 3)] = rb[i][j];
-                }
+            for (int j = 0; j < 4; ++j) {
+                const int n = 4 * (tid & 15) + j;
+                *reinterpret_cast<f32x4*>(&Bs[buf][n * kF32BK + swz8(n, kc) * 4]) =
+                    f32x4{rb[0][j], rb[1][j], rb[2][j], rb[3][j]};
             }
         }
     };
