@@ -426,8 +426,48 @@ def wl_engine_cfg1(torch, args):
     return res
 
 
+def _eltwise_line(name, config, nbytes, ms_step, ms_kernel):
+    return {
+        "value": nbytes / (ms_step * 1e-3) / 1e9, "unit": "GB/s", "ms_per_step": ms_step, "dtype": "bf16",
+        "config": config,
+        "roofline": {"bound": "hbm", "achieved": nbytes / (ms_kernel * 1e-3) / 1e9, "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": nbytes / (ms_kernel * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                     "traffic": load_traffic(name), "kernel_ms": ms_kernel,
+                     "algorithmic_bytes_per_launch": nbytes},
+    }
+
+
+def wl_gelu(torch, args):
+    """GELU (exact erf form) over 64 Mi bf16 elements, read once and written
+    once: 256 MiB of algorithmic HBM traffic per launch."""
+    import pyc_amd
+    n = 64 << 20
+    x = torch.randn(n, generator=torch.Generator(device="cuda").manual_seed(13), device="cuda").to(torch.bfloat16)
+    y = torch.empty_like(x)
+    ms_step, ms_kernel, _ = time_launches(torch, lambda: pyc_amd.gelu(x, y), args.steps, args.warmup)
+    return _eltwise_line("gelu", {"workload": "gelu_bf16_64Mi"}, 4.0 * n, ms_step, ms_kernel)
+
+
+def wl_layernorm(torch, args):
+    """LayerNorm over the last dimension of a [16384, 4096] bf16 tensor with
+    bf16 gamma/beta: x read, y written once (gamma/beta 16 KiB): 256 MiB of
+    algorithmic HBM traffic per launch."""
+    import pyc_amd
+    rows, D = 16384, 4096
+    g = torch.Generator(device="cuda").manual_seed(14)
+    x = (torch.randn((rows, D), generator=g, device="cuda") * 2 + 1).to(torch.bfloat16)
+    gamma = torch.randn(D, generator=g, device="cuda").to(torch.bfloat16)
+    beta = torch.randn(D, generator=g, device="cuda").to(torch.bfloat16)
+    y = torch.empty_like(x)
+    ms_step, ms_kernel, _ = time_launches(torch, lambda: pyc_amd.layernorm(x, y, gamma, beta), args.steps,
+                                          args.warmup)
+    return _eltwise_line("layernorm", {"workload": "layernorm_bf16_16384x4096_affine"},
+                         4.0 * rows * D + 4.0 * D, ms_step, ms_kernel)
+
+
 WORKLOADS = {"gemm_bf16": wl_gemm_bf16, "gemm_f32_cfg1": wl_gemm_f32_cfg1, "decode_chain": wl_decode_chain,
-             "attention": wl_attention, "conv": wl_conv, "engine_cfg1": wl_engine_cfg1}
+             "attention": wl_attention, "conv": wl_conv, "engine_cfg1": wl_engine_cfg1,
+             "gelu": wl_gelu, "layernorm": wl_layernorm}
 
 
 def main() -> int:

@@ -100,6 +100,22 @@ int pyc_hip_w8a16_chain_reserve(int M, int nsteps, const int* N, const int* K);
  * Synchronizes the device; clear != 0 resets the flag. */
 int pyc_hip_w8a16_chain_error(int clear);
 
+/* GELU, exact erf form: y = 0.5 x (1 + erf(x / sqrt(2))), elementwise over n
+ * elements (no reference kernel: the reference reports PYC_IR_OP_GELU as a
+ * graph break and executes it nowhere, reference
+ * src/compiler/passes/pass_manager.c:313-373). fp32 statistics, one rounding.
+ * Symbols "hip_gelu_f32", "hip_gelu_bf16", "hip_gelu_f16". 0, -1 (bad
+ * arguments), -2 (HIP error). */
+int pyc_hip_gelu_dispatch(const char* symbol, size_t n, const void* x, void* y, void* stream);
+
+/* LayerNorm over the last dimension of a [rows, D] row-major tensor:
+ * y = (x - mean) / sqrt(var + eps) * gamma + beta, var the population
+ * variance, gamma and beta [D] of x's type or NULL (1 and 0). Same reference
+ * status as GELU (PYC_IR_OP_LAYERNORM). Symbols "hip_layernorm_f32",
+ * "hip_layernorm_bf16", "hip_layernorm_f16". 0, -1, -2 as above. */
+int pyc_hip_layernorm_dispatch(const char* symbol, int rows, int D, float eps, const void* x, const void* gamma,
+                               const void* beta, void* y, void* stream);
+
 /* Device properties the bench and the registry report. */
 typedef struct {
     char gcn_arch[64];       /* e.g. "gfx950:sramecc+:xnack-" */

@@ -8,6 +8,9 @@ this package, and only as the checker. It wraps two native libraries:
   of fp32 reference attention / NHWC conv / fp8-weight GEMM.
 * ``_ref/libpyc_ref.so`` — the reference's own C11 engine compiled from
   /root/reference by ``Makefile.ref`` (present only where it was built).
+
+plus float64 numpy restatements of GELU and LayerNorm (ops the reference
+executes nowhere), pinned against torch in tests/test_oracle.py.
 """
 from __future__ import annotations
 
@@ -188,3 +191,27 @@ def w8a16_chain(x_bits, layers) -> np.ndarray:
         t = w8a16_layer(h, wq_up, s_up, True)
         h = w8a16_layer(t, wq_dn, s_dn, False)
     return h
+
+
+def gelu_f64(x: np.ndarray) -> np.ndarray:
+    """GELU, exact form 0.5 x (1 + erf(x / sqrt(2))), in float64 (the
+    reference defines no GELU: it is a graph break there; this is PyTorch's
+    default definition)."""
+    from scipy.special import erf
+    x = np.asarray(x, dtype=np.float64)
+    return 0.5 * x * (1.0 + erf(x / np.sqrt(2.0)))
+
+
+def layernorm_f64(x: np.ndarray, gamma=None, beta=None, eps: float = 1e-5) -> np.ndarray:
+    """LayerNorm over the last dimension in float64: (x - mean) / sqrt(var +
+    eps) * gamma + beta, var the population variance (as PyTorch's
+    layer_norm; the reference executes no LAYERNORM)."""
+    x = np.asarray(x, dtype=np.float64)
+    mean = x.mean(axis=-1, keepdims=True)
+    var = ((x - mean) ** 2).mean(axis=-1, keepdims=True)
+    y = (x - mean) / np.sqrt(var + eps)
+    if gamma is not None:
+        y = y * np.asarray(gamma, dtype=np.float64)
+    if beta is not None:
+        y = y + np.asarray(beta, dtype=np.float64)
+    return y

@@ -47,6 +47,10 @@ def _declare(L: C.CDLL) -> None:
     L.pyc_hip_w8a16_chain_reserve.restype = I
     L.pyc_hip_w8a16_chain_error.argtypes = [I]
     L.pyc_hip_w8a16_chain_error.restype = I
+    L.pyc_hip_gelu_dispatch.argtypes = [S, Z, P, P, P]
+    L.pyc_hip_gelu_dispatch.restype = I
+    L.pyc_hip_layernorm_dispatch.argtypes = [S, I, I, F, P, P, P, P, P]
+    L.pyc_hip_layernorm_dispatch.restype = I
     L.pyc_hip_device_query.argtypes = [C.POINTER(abi.DeviceInfo)]
     L.pyc_hip_device_query.restype = I
     L.pyc_hip_kernel_symbol_count.argtypes = [S]
@@ -186,6 +190,26 @@ def w8a16_chain_reserve(M: int, layers) -> None:
 def w8a16_chain_error(clear: bool = True) -> int:
     """1 if a chain launch timed out waiting (output invalid), else 0."""
     return lib().pyc_hip_w8a16_chain_error(int(clear))
+
+
+def _elt_suffix(t) -> str:
+    import torch
+    return {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16"}[t.dtype]
+
+
+def gelu(x, y, stream=None) -> None:
+    """y = GELU(x), exact erf form, elementwise (same dtype and element count)."""
+    _check(lib().pyc_hip_gelu_dispatch(_b("hip_gelu_" + _elt_suffix(x)), x.numel(), _ptr(x), _ptr(y),
+                                       _stream(stream)), "gelu")
+
+
+def layernorm(x, y, gamma=None, beta=None, eps: float = 1e-5, stream=None) -> None:
+    """y = LayerNorm(x) over the last dimension, optional gamma/beta [D] of x's type."""
+    D = x.shape[-1]
+    _check(lib().pyc_hip_layernorm_dispatch(_b("hip_layernorm_" + _elt_suffix(x)), x.numel() // D, D, eps,
+                                            _ptr(x), _ptr(gamma) if gamma is not None else None,
+                                            _ptr(beta) if beta is not None else None, _ptr(y),
+                                            _stream(stream)), "layernorm")
 
 
 def device_info() -> abi.DeviceInfo:

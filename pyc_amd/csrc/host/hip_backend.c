@@ -190,7 +190,7 @@ static size_t shape_elems(const pyc_shape* s) {
     return n;
 }
 
-enum { ST_GEMM = 1, ST_W8A16 = 2, ST_CONV = 3, ST_ATTN = 4 };
+enum { ST_GEMM = 1, ST_W8A16 = 2, ST_CONV = 3, ST_ATTN = 4, ST_GELU = 5, ST_LAYERNORM = 6 };
 enum { ADD_NONE = 0, ADD_MATRIX = 1, ADD_ROW_BIAS = 2, ADD_SCALAR = 3 };
 
 typedef struct {
@@ -204,6 +204,8 @@ typedef struct {
     int m, n, k;  /* GEMM dims */
     int conv[11]; /* N H W C K R S ph pw sh sw */
     int attn[5];  /* B H S D causal */
+    size_t elems; /* GELU: elements; LAYERNORM: rows (m) x last dim (n) */
+    float eps;    /* LAYERNORM epsilon */
     char symbol[PYC_KERNEL_SYMBOL_MAX];
 } hip_step;
 
@@ -585,6 +587,68 @@ static int build_plan(const pyc_ir_module* m, hip_plan* plan) {
                 plan->nsteps++;
                 break;
             }
+            case PYC_IR_OP_GELU:
+            case PYC_IR_OP_LAYERNORM: {
+                /* GELU (exact erf form) elementwise; LAYERNORM over the last
+                 * dimension with optional gamma (input 1) and beta (input 2)
+                 * of shape [D] and x's type, epsilon 1e-5 or "@eps<value>" in
+                 * the op name. The reference executes neither (its pass
+                 * report counts them as graph breaks, reference
+                 * src/compiler/passes/pass_manager.c:313-373). */
+                const int is_ln = op->kind == PYC_IR_OP_LAYERNORM;
+                int x = op->input_count >= 1 ? op->input_ids[0] : -1;
+                size_t k;
+                if (!valid_id(m, x) || x >= (int)i || op->input_count > (is_ln ? 3u : 1u)) {
+                    return 1;
+                }
+                x = plan->value_op[x];
+                if (plan->value_bytes[x] == 0 || (plan->vdtype[x] != PYC_DTYPE_F32 && plan->vdtype[x] != PYC_DTYPE_BF16 &&
+                                                  plan->vdtype[x] != PYC_DTYPE_F16)) {
+                    return 1;
+                }
+                memset(st, 0, sizeof(*st));
+                st->kind = is_ln ? ST_LAYERNORM : ST_GELU;
+                st->dtype = plan->vdtype[x];
+                st->out = (int)i;
+                st->in[0] = x;
+                st->in[1] = st->in[2] = -1;
+                st->add_in = -1;
+                st->elems = shape_elems(&plan->vshape[x]);
+                if (is_ln) {
+                    const pyc_shape* xs = &plan->vshape[x];
+                    const char* e = strstr(op->name, "@eps");
+                    if (xs->rank < 1 || xs->dims[xs->rank - 1] <= 0 || xs->dims[xs->rank - 1] > 0x7FFFFFFF) {
+                        return 1;
+                    }
+                    st->n = (int)xs->dims[xs->rank - 1];
+                    if (st->elems / (size_t)st->n > 0x7FFFFFFF) {
+                        return 1;
+                    }
+                    st->m = (int)(st->elems / (size_t)st->n);
+                    st->eps = e ? strtof(e + 4, NULL) : 1e-5f;
+                    if (!(st->eps >= 0.0f)) {
+                        return 1;
+                    }
+                    for (k = 1; k < op->input_count; ++k) {
+                        int gb = op->input_ids[k];
+                        if (!valid_id(m, gb) || gb >= (int)i) {
+                            return 1;
+                        }
+                        gb = plan->value_op[gb];
+                        if (plan->vdtype[gb] != st->dtype || shape_elems(&plan->vshape[gb]) != (size_t)st->n) {
+                            return 1;
+                        }
+                        st->in[k] = gb;
+                    }
+                }
+                set_reason(st->symbol, sizeof(st->symbol),
+                           st->dtype == PYC_DTYPE_F32 ? (is_ln ? "hip_layernorm_f32" : "hip_gelu_f32")
+                           : st->dtype == PYC_DTYPE_BF16 ? (is_ln ? "hip_layernorm_bf16" : "hip_gelu_bf16")
+                                                          : (is_ln ? "hip_layernorm_f16" : "hip_gelu_f16"));
+                set_value(plan, (int)i, &plan->vshape[x], st->dtype);
+                plan->nsteps++;
+                break;
+            }
             case PYC_IR_OP_OUTPUT: {
                 int src = op->input_count >= 1 ? op->input_ids[0] : -1;
                 if (!valid_id(m, src) || src >= (int)i || plan->n_outputs >= 64) {
@@ -598,7 +662,7 @@ static int build_plan(const pyc_ir_module* m, hip_plan* plan) {
                 break;
             }
             default:
-                return 1; /* ADD/RELU not absorbed, CONST, GELU, REDUCE_SUM, LAYERNORM */
+                return 1; /* ADD/RELU not absorbed, CONST, REDUCE_SUM */
         }
     }
     return 0;
@@ -874,6 +938,14 @@ static int enqueue_steps(const pyc_ir_module* m, const hip_plan* plan, void* con
                                              st->conv[4], st->conv[5], st->conv[6], st->conv[7], st->conv[8],
                                              st->conv[9], st->conv[10], vp[st->in[0]],
                                              vp[st->in[1]], bias, st->relu, out, st_stream);
+                break;
+            case ST_GELU:
+                rc = pyc_hip_gelu_dispatch(st->symbol, st->elems, vp[st->in[0]], out, st_stream);
+                break;
+            case ST_LAYERNORM:
+                rc = pyc_hip_layernorm_dispatch(st->symbol, st->m, st->n, st->eps, vp[st->in[0]],
+                                                st->in[1] >= 0 ? vp[st->in[1]] : NULL,
+                                                st->in[2] >= 0 ? vp[st->in[2]] : NULL, out, st_stream);
                 break;
             case ST_ATTN: {
                 const float scale = 1.0f / sqrtf((float)st->attn[3]);
@@ -1407,6 +1479,8 @@ static int native_kind_supported(const pyc_ir_module* m) {
             case PYC_IR_OP_OUTPUT:
             case PYC_IR_OP_CONV2D:
             case PYC_IR_OP_ATTENTION:
+            case PYC_IR_OP_GELU:
+            case PYC_IR_OP_LAYERNORM:
                 break;
             default:
                 return 0;

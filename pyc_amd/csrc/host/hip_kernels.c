@@ -39,10 +39,13 @@ int pyc_hip_w8a16_launch(int M, int N, int K, const void* X, const void* Wq, con
 int pyc_hip_w8a16_chain_launch(int M, int nsteps, const void* X, const void* const* Wq,
                                const float* const* scale, const int* N, const int* K, const int* relu,
                                void* Y, void* stream);
+int pyc_hip_gelu_launch(int dtype, size_t n, const void* x, void* y, void* stream);
+int pyc_hip_layernorm_launch(int dtype, int rows, int D, float eps, const void* x, const void* gamma,
+                             const void* beta, void* y, void* stream);
 
 /* ---------------------------------------------------------------- variant table */
 
-enum { VK_GEMM = 1, VK_ATTN = 2, VK_CONV = 3, VK_W8 = 4 };
+enum { VK_GEMM = 1, VK_ATTN = 2, VK_CONV = 3, VK_W8 = 4, VK_ELT = 5 };
 enum { VT_BF16 = 1, VT_F16 = 2, VT_F32 = 3 };
 
 typedef struct {
@@ -94,6 +97,13 @@ static const hip_variant k_variants[] = {
     {"conv2d", "cutlass_conv2d_fprop_bf16", VK_CONV, VT_BF16, 0, 0, 0, 90, 0.125, 131072, 2, PYC_KERNEL_WORKLOAD_ANY},
     /* weight-only fp8 decode GEMM (no reference counterpart) */
     {"matmul_w8a16", "hip_gemm_w8a16_e4m3", VK_W8, VT_BF16, 1, 0, 0, 100, 0.5, 16384, 2, PYC_KERNEL_WORKLOAD_WIDE_SKINNY},
+    /* GELU / LayerNorm, the reference's graph-break ops (no reference kernel) */
+    {"gelu", "hip_gelu_f32", VK_ELT, VT_F32, 0, 0, 0, 100, 1.0, 0, 1, PYC_KERNEL_WORKLOAD_ANY},
+    {"gelu", "hip_gelu_bf16", VK_ELT, VT_BF16, 0, 0, 0, 100, 1.0, 0, 1, PYC_KERNEL_WORKLOAD_ANY},
+    {"gelu", "hip_gelu_f16", VK_ELT, VT_F16, 0, 0, 0, 100, 1.0, 0, 1, PYC_KERNEL_WORKLOAD_ANY},
+    {"layernorm", "hip_layernorm_f32", VK_ELT, VT_F32, 0, 0, 0, 100, 1.0, 0, 1, PYC_KERNEL_WORKLOAD_ANY},
+    {"layernorm", "hip_layernorm_bf16", VK_ELT, VT_BF16, 0, 0, 0, 100, 1.0, 0, 1, PYC_KERNEL_WORKLOAD_ANY},
+    {"layernorm", "hip_layernorm_f16", VK_ELT, VT_F16, 0, 0, 0, 100, 1.0, 0, 1, PYC_KERNEL_WORKLOAD_ANY},
 };
 
 static const hip_variant* find_variant(const char* symbol, int kind) {
@@ -239,6 +249,28 @@ int pyc_hip_w8a16_chain_dispatch(const char* symbol, int M, int nsteps, const vo
     return rc == -3 ? -1 : rc;
 }
 
+/* ---------------------------------------------------------------- GELU / LayerNorm */
+
+static int elt_dtype(const hip_variant* v) { return v->dtype == VT_F32 ? 0 : v->dtype == VT_BF16 ? 1 : 2; }
+
+int pyc_hip_gelu_dispatch(const char* symbol, size_t n, const void* x, void* y, void* stream) {
+    const hip_variant* v = find_variant(symbol, VK_ELT);
+    if (!v || strcmp(v->op_key, "gelu") != 0 || (n > 0 && (!x || !y))) {
+        return -1;
+    }
+    return pyc_hip_gelu_launch(elt_dtype(v), n, x, y, stream);
+}
+
+int pyc_hip_layernorm_dispatch(const char* symbol, int rows, int D, float eps, const void* x, const void* gamma,
+                               const void* beta, void* y, void* stream) {
+    const hip_variant* v = find_variant(symbol, VK_ELT);
+    if (!v || strcmp(v->op_key, "layernorm") != 0 || rows < 0 || D <= 0 || !(eps >= 0.0f) ||
+        (rows > 0 && (!x || !y))) {
+        return -1;
+    }
+    return pyc_hip_layernorm_launch(elt_dtype(v), rows, D, eps, x, gamma, beta, y, stream);
+}
+
 /* ---------------------------------------------------------------- registry */
 
 static pyc_mutex g_registry_init_lock = PYC_MUTEX_INIT;
@@ -262,7 +294,7 @@ void pyc_cutlass_registry_init(void) {
             d.backend = PYC_BACKEND_CUDA;
             d.priority = v->priority;
             d.estimated_occupancy = v->occupancy;
-            d.tensor_core_eligible = 1;
+            d.tensor_core_eligible = v->kind != VK_ELT;  /* GELU/LayerNorm: VALU only */
             d.shared_mem_bytes = v->lds_bytes;
             d.reg_pressure_class = v->reg_class;
             d.preferred_workload_family = v->workload;

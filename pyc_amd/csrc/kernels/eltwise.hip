@@ -1,0 +1,271 @@
+// eltwise.hip — GELU and LayerNorm on gfx950: the IR's PYC_IR_OP_GELU and
+// PYC_IR_OP_LAYERNORM, which the reference engine reports as graph breaks and
+// executes nowhere (its CPU executor rejects them, reference
+// src/compiler/compiler_api.c:1877-2092; its GPU path accepts matmul chains
+// only, reference src/compiler/runtime/cuda_backend.c:1201-1390; the break
+// accounting is reference src/compiler/passes/pass_manager.c:313-373).
+// Semantics chosen here, as PyTorch defines them:
+//   GELU(x)      = 0.5 x (1 + erf(x / sqrt(2)))               (exact form)
+//   LayerNorm(x) = (x - mean) / sqrt(var + eps) * gamma + beta over the last
+//                  dimension, var the population variance (divide by D).
+// Both are HBM-bound. Elements are fp32, bf16 or fp16; every statistic and
+// every intermediate is fp32, results are rounded once (to nearest even).
+#include <math.h>
+
+#include <type_traits>
+
+#include "common.hpp"
+
+namespace pyc {
+
+template <typename T> struct io;
+template <> struct io<float> {
+    static constexpr int kVec = 4;  // elements per 16-byte chunk
+    __device__ static inline float get(const float* p, size_t i) { return p[i]; }
+    __device__ static inline void put(float* p, size_t i, float v) { p[i] = v; }
+    __device__ static inline void get16(const float* p, size_t i, float (&v)[4]) {
+        const f32x4 c = *reinterpret_cast<const f32x4*>(p + i);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = c[e];
+    }
+    __device__ static inline void put16(float* p, size_t i, const float (&v)[4]) {
+        *reinterpret_cast<f32x4*>(p + i) = f32x4{v[0], v[1], v[2], v[3]};
+    }
+};
+template <typename H> struct io_half {
+    static constexpr int kVec = 8;
+    __device__ static inline float get(const uint16_t* p, size_t i) { return elem<H>::to_f32(p[i]); }
+    __device__ static inline void put(uint16_t* p, size_t i, float v) { p[i] = elem<H>::from_f32(v); }
+    __device__ static inline void get16(const uint16_t* p, size_t i, float (&v)[8]) {
+        const u32x4 c = *reinterpret_cast<const u32x4*>(p + i);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[2 * e] = elem<H>::to_f32((uint16_t)(c[e] & 0xFFFFu));
+            v[2 * e + 1] = elem<H>::to_f32((uint16_t)(c[e] >> 16));
+        }
+    }
+    __device__ static inline void put16(uint16_t* p, size_t i, const float (&v)[8]) {
+        u32x4 c;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            c[e] = (uint32_t)elem<H>::from_f32(v[2 * e]) | ((uint32_t)elem<H>::from_f32(v[2 * e + 1]) << 16);
+        *reinterpret_cast<u32x4*>(p + i) = c;
+    }
+};
+template <> struct io<bf16_t> : io_half<bf16_t> {};
+template <> struct io<f16_t> : io_half<f16_t> {};
+
+// storage type of T in memory
+template <typename T> using store_t = typename std::conditional<std::is_same<T, float>::value, float, uint16_t>::type;
+
+__device__ inline float gelu_f(float x) { return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f)); }
+
+// Grid-stride over 16-byte chunks; the n % kVec tail (and unaligned tensors)
+// by elements.
+template <typename T>
+__global__ void __launch_bounds__(256) gelu_kernel(const store_t<T>* __restrict__ x, store_t<T>* __restrict__ y,
+                                                   size_t n, int vec_ok) {
+    using IO = io<T>;
+    constexpr int V = IO::kVec;
+    const size_t tid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    const size_t nchunks = vec_ok ? n / V : 0;
+    // four chunks per thread and iteration, all loads issued before the erf work
+    for (size_t c0 = tid; c0 < nchunks; c0 += 4 * stride) {
+        float v[4][V];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (c0 + u * stride < nchunks) IO::get16(x, (c0 + u * stride) * V, v[u]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (c0 + u * stride < nchunks) {
+#pragma unroll
+                for (int e = 0; e < V; ++e) v[u][e] = gelu_f(v[u][e]);
+                IO::put16(y, (c0 + u * stride) * V, v[u]);
+            }
+        }
+    }
+    for (size_t i = nchunks * V + tid; i < n; i += stride) IO::put(y, i, gelu_f(IO::get(x, i)));
+}
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+// One wave per row, four rows per workgroup. Three passes over the row (sum,
+// sum of squared deviations, normalize): the second and third read it from
+// the caches; the two-pass variance has no cancellation for rows whose mean
+// is large against their spread.
+template <typename T, bool VEC>
+__global__ void __launch_bounds__(256) layernorm_kernel(const store_t<T>* __restrict__ x,
+                                                        const store_t<T>* __restrict__ gamma,
+                                                        const store_t<T>* __restrict__ beta,
+                                                        store_t<T>* __restrict__ y, int rows, int D, float eps) {
+    using IO = io<T>;
+    constexpr int V = VEC ? IO::kVec : 1;
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const store_t<T>* xr = x + (size_t)row * D;
+    store_t<T>* yr = y + (size_t)row * D;
+    const int nch = D / V;
+    auto chunk = [&](const store_t<T>* p, int c, float (&v)[V]) {
+        if constexpr (VEC) IO::get16(p, (size_t)c * V, v);
+        else v[0] = IO::get(p, (size_t)c);
+    };
+    float s = 0.f;
+    for (int c = lane; c < nch; c += kWave) {
+        float v[V];
+        chunk(xr, c, v);
+#pragma unroll
+        for (int e = 0; e < V; ++e) s += v[e];
+    }
+    const float mean = wave_sum(s) / (float)D;
+    float s2 = 0.f;
+    for (int c = lane; c < nch; c += kWave) {
+        float v[V];
+        chunk(xr, c, v);
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+            const float d = v[e] - mean;
+            s2 += d * d;
+        }
+    }
+    const float rstd = 1.0f / sqrtf(wave_sum(s2) / (float)D + eps);
+    for (int c = lane; c < nch; c += kWave) {
+        float v[V], g[V], b[V];
+        chunk(xr, c, v);
+        if (gamma) chunk(gamma, c, g);
+        if (beta) chunk(beta, c, b);
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+            float o = (v[e] - mean) * rstd;
+            if (gamma) o *= g[e];
+            if (beta) o += b[e];
+            v[e] = o;
+        }
+        if constexpr (VEC) IO::put16(yr, (size_t)c * V, v);
+        else IO::put(yr, (size_t)c, v[0]);
+    }
+}
+
+// Rows of at most kLnRegChunks 16-byte chunks per lane (D <= 4096 bf16/fp16,
+// 2048 fp32) whose D is a multiple of 64 chunks: the row is read once into
+// registers, both statistics come from the registers, and it is written once.
+constexpr int kLnRegChunks = 8;
+template <typename T>
+__global__ void __launch_bounds__(256) layernorm_reg_kernel(const store_t<T>* __restrict__ x,
+                                                            const store_t<T>* __restrict__ gamma,
+                                                            const store_t<T>* __restrict__ beta,
+                                                            store_t<T>* __restrict__ y, int rows, int D, float eps) {
+    using IO = io<T>;
+    constexpr int V = IO::kVec;
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const store_t<T>* xr = x + (size_t)row * D;
+    store_t<T>* yr = y + (size_t)row * D;
+    const int nc = D / (V * kWave);  // chunks per lane, 1..kLnRegChunks
+    float v[kLnRegChunks][V];
+#pragma unroll
+    for (int j = 0; j < kLnRegChunks; ++j)
+        if (j < nc) IO::get16(xr, (size_t)(j * kWave + lane) * V, v[j]);
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < kLnRegChunks; ++j)
+        if (j < nc) {
+#pragma unroll
+            for (int e = 0; e < V; ++e) s += v[j][e];
+        }
+    const float mean = wave_sum(s) / (float)D;
+    float s2 = 0.f;
+#pragma unroll
+    for (int j = 0; j < kLnRegChunks; ++j)
+        if (j < nc) {
+#pragma unroll
+            for (int e = 0; e < V; ++e) {
+                const float d = v[j][e] - mean;
+                s2 += d * d;
+            }
+        }
+    const float rstd = 1.0f / sqrtf(wave_sum(s2) / (float)D + eps);
+#pragma unroll
+    for (int j = 0; j < kLnRegChunks; ++j)
+        if (j < nc) {
+            const size_t off = (size_t)(j * kWave + lane) * V;
+            float g[V], b[V];
+            if (gamma) IO::get16(gamma, off, g);
+            if (beta) IO::get16(beta, off, b);
+#pragma unroll
+            for (int e = 0; e < V; ++e) {
+                float o = (v[j][e] - mean) * rstd;
+                if (gamma) o *= g[e];
+                if (beta) o += b[e];
+                v[j][e] = o;
+            }
+            IO::put16(yr, off, v[j]);
+        }
+}
+
+template <typename T>
+static int launch_gelu(const void* x, void* y, size_t n, hipStream_t s) {
+    constexpr int V = io<T>::kVec;
+    const int vec_ok = ((((uintptr_t)x | (uintptr_t)y) & 15) == 0) ? 1 : 0;
+    const size_t work = vec_ok ? (n + V - 1) / V : n;
+    size_t blocks = (work + 255) / 256;
+    if (blocks > 256 * 16) blocks = 256 * 16;  // 16 workgroups per CU, grid-stride beyond
+    if (blocks == 0) blocks = 1;
+    hipLaunchKernelGGL(gelu_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, s, (const store_t<T>*)x,
+                       (store_t<T>*)y, n, vec_ok);
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+template <typename T>
+static int launch_layernorm(const void* x, const void* g, const void* b, void* y, int rows, int D, float eps,
+                            hipStream_t s) {
+    constexpr int V = io<T>::kVec;
+    const bool vec = D % V == 0 && ((((uintptr_t)x | (uintptr_t)y | (uintptr_t)g | (uintptr_t)b) & 15) == 0);
+    const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+    if (vec && D % (V * kWave) == 0 && D / (V * kWave) <= kLnRegChunks)
+        hipLaunchKernelGGL(layernorm_reg_kernel<T>, grid, block, 0, s, (const store_t<T>*)x, (const store_t<T>*)g,
+                           (const store_t<T>*)b, (store_t<T>*)y, rows, D, eps);
+    else if (vec)
+        hipLaunchKernelGGL((layernorm_kernel<T, true>), grid, block, 0, s, (const store_t<T>*)x,
+                           (const store_t<T>*)g, (const store_t<T>*)b, (store_t<T>*)y, rows, D, eps);
+    else
+        hipLaunchKernelGGL((layernorm_kernel<T, false>), grid, block, 0, s, (const store_t<T>*)x,
+                           (const store_t<T>*)g, (const store_t<T>*)b, (store_t<T>*)y, rows, D, eps);
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+}  // namespace pyc
+
+// dtype: 0 fp32, 1 bf16, 2 fp16. 0, -1 (bad arguments), -2 (HIP error).
+extern "C" int pyc_hip_gelu_launch(int dtype, size_t n, const void* x, void* y, void* stream) {
+    using namespace pyc;
+    if (n == 0) return 0;
+    if (!x || !y) return -1;
+    hipStream_t s = (hipStream_t)stream;
+    switch (dtype) {
+        case 0: return launch_gelu<float>(x, y, n, s);
+        case 1: return launch_gelu<bf16_t>(x, y, n, s);
+        case 2: return launch_gelu<f16_t>(x, y, n, s);
+        default: return -1;
+    }
+}
+
+extern "C" int pyc_hip_layernorm_launch(int dtype, int rows, int D, float eps, const void* x, const void* gamma,
+                                        const void* beta, void* y, void* stream) {
+    using namespace pyc;
+    if (rows == 0) return 0;
+    if (rows < 0 || D <= 0 || !x || !y || !(eps >= 0.f)) return -1;
+    hipStream_t s = (hipStream_t)stream;
+    switch (dtype) {
+        case 0: return launch_layernorm<float>(x, gamma, beta, y, rows, D, eps, s);
+        case 1: return launch_layernorm<bf16_t>(x, gamma, beta, y, rows, D, eps, s);
+        case 2: return launch_layernorm<f16_t>(x, gamma, beta, y, rows, D, eps, s);
+        default: return -1;
+    }
+}

@@ -300,3 +300,48 @@ def test_w8a16_layer_vs_fp64():
         exp = np.maximum(ref, 0) if relu else ref
         # one bf16 rounding of the result: half an ulp, 2^-9 relative
         np.testing.assert_allclose(got, exp, rtol=2.0 ** -8, atol=1e-6)
+
+
+def test_gelu_oracle_pinned():
+    """oracle.gelu_f64 against torch's exact-erf GELU in float64, and identities
+    a wrong sign or constant in the erf argument breaks: GELU(0) = 0,
+    GELU(x) - GELU(-x) = x, GELU(x) -> x for large x and -> 0 for very negative x."""
+    import torch
+
+    r = np.random.default_rng(11)
+    x = np.concatenate([r.standard_normal(4096) * 3.0, [0.0, -40.0, 40.0, 1e-7, -1e-7]])
+    got = oracle.gelu_f64(x)
+    ref = torch.nn.functional.gelu(torch.from_numpy(x), approximate="none").numpy()
+    assert np.max(np.abs(got - ref)) <= 1e-14 * np.max(np.abs(ref))
+    assert oracle.gelu_f64(np.array([0.0]))[0] == 0.0
+    assert np.allclose(oracle.gelu_f64(x) - oracle.gelu_f64(-x), x, rtol=0, atol=1e-12)
+    assert abs(oracle.gelu_f64(np.array([40.0]))[0] - 40.0) < 1e-12
+    assert abs(oracle.gelu_f64(np.array([-40.0]))[0]) < 1e-12
+    # Phi(1) = 0.8413447460685429 (standard normal CDF)
+    assert abs(oracle.gelu_f64(np.array([1.0]))[0] - 0.8413447460685429) < 1e-15
+
+
+def test_layernorm_oracle_pinned():
+    """oracle.layernorm_f64 against torch's layer_norm in float64 (with and
+    without affine, two epsilons), and what the definition fixes: without
+    affine each row has mean 0 and variance var/(var+eps); a row of equal
+    values maps to beta; gamma and beta act per column."""
+    import torch
+
+    r = np.random.default_rng(12)
+    x = r.standard_normal((37, 300)) * 2.5 + 7.0
+    g = r.standard_normal(300)
+    b = r.standard_normal(300)
+    for eps in (1e-5, 1e-2):
+        for gg, bb in ((None, None), (g, b)):
+            got = oracle.layernorm_f64(x, gg, bb, eps)
+            ref = torch.nn.functional.layer_norm(torch.from_numpy(x), (300,),
+                                                 None if gg is None else torch.from_numpy(gg),
+                                                 None if bb is None else torch.from_numpy(bb), eps).numpy()
+            assert np.max(np.abs(got - ref)) <= 1e-12
+    y = oracle.layernorm_f64(x, eps=1e-5)
+    var = x.var(axis=1)
+    assert np.allclose(y.mean(axis=1), 0.0, atol=1e-12)
+    assert np.allclose(y.var(axis=1), var / (var + 1e-5), rtol=1e-12)
+    const = np.full((2, 300), 3.25)
+    assert np.allclose(oracle.layernorm_f64(const, g, b), b[None, :], atol=1e-12)
