@@ -39,6 +39,18 @@ int pyc_hip_gemm_dispatch(
     const float* bias, int epilogue,
     void* stream);
 
+/* Measured autotune of the [M,K]x[K,N] GEMM at a live shape (the reference's
+ * compiler_api.c:3000-3044 records one estimated candidate per run instead):
+ * every registered variant of `dtype` (PYC_DTYPE_F32/BF16/F16) whose right
+ * operand is [K,N] is launched `iters` times on scratch operands and timed
+ * by HIP events; the fastest becomes the symbol the backend plans for GEMMs
+ * of that dtype and shape. Writes up to `cap` symbols (each in a slot of
+ * `sym_stride` bytes of `syms`) and their mean ms. Returns the number timed,
+ * 0 without a GPU, -1 on bad arguments. */
+int pyc_hip_autotune_gemm(
+    pyc_dtype dtype, int M, int N, int K, int iters,
+    char* syms, size_t sym_stride, double* ms, int cap);
+
 /* Generalises reference attention/kernel.cu:95-122 to batch and heads:
  * O[b,h] = softmax(Q[b,h] K[b,h]^T * scale (+ causal mask)) V[b,h],
  * Q,K,V,O [B,H,S,D] contiguous (BHSD), fp32 softmax and accumulation.

@@ -39,6 +39,7 @@
 #include <unistd.h>
 
 #include "pyc/cuda_backend.h"
+#include "pyc/hip_backend.h"
 #include "pyc/kernel_registry.h"
 #include "pyc/pass_manager.h"
 #include "pyc/runtime_allocator.h"
@@ -104,6 +105,7 @@ struct pyc_compiled_model {
     char autotune_db[512];
     int autotune_loaded;
     int autotune_saved;
+    int hip_tuned; /* measured autotune done for this model's GEMM */
     pyc_kernel_desc candidates[CANDIDATE_MAX];
     size_t candidate_count;
     size_t run_count;
@@ -962,6 +964,50 @@ static int autotune_persist(const char* path, const char* op, pyc_backend backen
     return rc;
 }
 
+/* On the GPU backend the first run with enable_autotune measures every
+ * registered tile variant of the module's first [M,K]x[K,N] GEMM at its live
+ * shape (pyc_hip_autotune_gemm, HIP-event timings). Each result updates the
+ * registry's "matmul" entry of that symbol and is persisted as an
+ * `matmul_fused|backend|symbol|best_ms` line; the fastest is promoted and
+ * becomes the plan's symbol for that shape. Without a GPU nothing is timed
+ * and the per-run estimate below stays in force. */
+static void measured_autotune(pyc_compiled_model* model, const pyc_ir_module* m) {
+    char syms[16][PYC_KERNEL_SYMBOL_MAX];
+    double ms[16];
+    size_t i;
+    int n, j, best = 0;
+    for (i = 0; i < m->op_count; ++i) {
+        const pyc_ir_op* op = &m->ops[i];
+        const pyc_ir_op *a, *b;
+        if (op->kind != PYC_IR_OP_MATMUL || op->input_count < 2 || op->input_ids[0] < 0 || op->input_ids[1] < 0 ||
+            (size_t)op->input_ids[0] >= m->op_count || (size_t)op->input_ids[1] >= m->op_count) {
+            continue;
+        }
+        a = &m->ops[op->input_ids[0]];
+        b = &m->ops[op->input_ids[1]];
+        if (a->shape.rank != 2 || b->shape.rank != 2 || a->shape.dims[1] != b->shape.dims[0] || a->dtype != b->dtype) {
+            return;
+        }
+        n = pyc_hip_autotune_gemm(a->dtype, (int)a->shape.dims[0], (int)b->shape.dims[1], (int)a->shape.dims[1], 10,
+                                  &syms[0][0], PYC_KERNEL_SYMBOL_MAX, ms, 16);
+        if (n <= 0) {
+            return;
+        }
+        for (j = 0; j < n; ++j) {
+            (void)pyc_kernel_benchmark_update_symbol("matmul", model->backend, syms[j], ms[j]);
+            if (autotune_persist(model->autotune_db, "matmul_fused", model->backend, syms[j], ms[j]) == 0) {
+                model->autotune_saved = 1;
+            }
+            if (ms[j] < ms[best]) {
+                best = j;
+            }
+        }
+        (void)pyc_kernel_promote_symbol("matmul", model->backend, syms[best]);
+        model->hip_tuned = 1;
+        return;
+    }
+}
+
 /* Heuristic time of a not-measured candidate (reference compiler_api.c:562-589);
  * used only on the CPU backend, where no device timing exists. */
 static double estimate_ms(double base, const pyc_kernel_desc* c, pyc_objective_mode mode, double pressure) {
@@ -1430,6 +1476,9 @@ pyc_status pyc_run_model(pyc_compiled_model* model, const pyc_tensor* inputs, si
         model->spec_guard_misses++;
     }
 
+    if (!error && model->backend == PYC_BACKEND_CUDA && model->options.enable_autotune && !model->hip_tuned) {
+        measured_autotune(model, exec);
+    }
     pyc_cuda_dispatch_trace_init(&model->trace);
     {
         const double t0 = now_ms();
@@ -1526,7 +1575,7 @@ pyc_status pyc_run_model(pyc_compiled_model* model, const pyc_tensor* inputs, si
     model->guard_misses += guard_miss;
     model->fallbacks += fallback;
 
-    if (!error && model->options.enable_autotune) {
+    if (!error && model->options.enable_autotune && !model->hip_tuned) {
         pyc_kernel_desc cand;
         double ms;
         model->candidate_count = pyc_kernel_collect("matmul_fused", model->backend, model->candidates, CANDIDATE_MAX);

@@ -60,6 +60,29 @@ int pyc_hip_w8a16_reserve(int N, int K);
 
 static pyc_mutex g_dispatch_lock = PYC_MUTEX_INIT;
 
+/* Measured GEMM tile choice per (dtype, M, N, K), filled by
+ * pyc_hip_autotune_gemm and read by build_plan; g_tune_gen is part of the
+ * graph signature so a new choice recaptures. */
+typedef struct {
+    pyc_dtype dtype;
+    int m, n, k;
+    char symbol[PYC_KERNEL_SYMBOL_MAX];
+} tuned_gemm;
+#define TUNED_MAX 32
+static tuned_gemm g_tuned[TUNED_MAX];
+static int g_tuned_count;
+static uint64_t g_tune_gen;
+
+static const char* tuned_symbol(pyc_dtype t, int m, int n, int k) {
+    int i;
+    for (i = 0; i < g_tuned_count; ++i) {
+        if (g_tuned[i].dtype == t && g_tuned[i].m == m && g_tuned[i].n == n && g_tuned[i].k == k) {
+            return g_tuned[i].symbol;
+        }
+    }
+    return NULL;
+}
+
 /* ---------------------------------------------------------------- env */
 
 static int env_true(const char* name) {
@@ -457,6 +480,9 @@ static int build_plan(const pyc_ir_module* m, hip_plan* plan) {
                         plan->is_weight[b] = 1;
                     }
                     set_reason(st->symbol, sizeof(st->symbol), default_gemm_symbol(t));
+                    if (tuned_symbol(t, st->m, st->n, st->k)) {
+                        set_reason(st->symbol, sizeof(st->symbol), tuned_symbol(t, st->m, st->n, st->k));
+                    }
                     if (t == PYC_DTYPE_F32 && env_true("PYC_CUDA_ENABLE_PROMOTED_GEMM")) {
                         char promoted[PYC_KERNEL_SYMBOL_MAX];
                         if (pyc_kernel_promoted_symbol("matmul", PYC_BACKEND_CUDA, promoted, sizeof(promoted)) == 0 &&
@@ -1134,6 +1160,7 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
     sig = fnv(sig, &m->op_count, sizeof(m->op_count));
     sig = fnv(sig, m->ops, m->op_count * sizeof(pyc_ir_op));
     sig = fnv(sig, &skip_out, sizeof(skip_out));
+    sig = fnv(sig, &g_tune_gen, sizeof(g_tune_gen));
     for (i = 0; i < m->op_count; ++i) {
         if (plan.input_ordinal[i] >= 0) {
             sig = fnv(sig, &copy_in[i], sizeof(int));
@@ -1606,6 +1633,103 @@ pyc_cuda_dispatch_status pyc_cuda_dispatch(const pyc_ir_module* module, const py
 }
 
 /* Releases every device/pinned buffer, the stream and the captured graph. */
+/* Measured autotune of the [M,K]x[K,N] GEMM (reference compiler_api.c:3000-3044
+ * records an estimate per run instead): every registered variant of the dtype
+ * with a [K,N] right operand is launched `iters` times at the live shape on
+ * scratch operands, timed by HIP events, and the fastest becomes the plan's
+ * symbol for that shape. Returns the number of timed variants (symbols and
+ * mean ms in syms/ms), 0 when nothing could be timed, -1 on bad arguments. */
+int pyc_hip_autotune_gemm(pyc_dtype dtype, int M, int N, int K, int iters, char* syms, size_t sym_stride,
+                          double* ms, int cap) {
+    static const char* const cands[] = {"hip_gemm_bf16_nn_256x256", "hip_gemm_bf16_nn_128x128", "hip_gemm_bf16_nn",
+                                        "cutlass_gemm_tensorcore_bf16", "hip_gemm_f16_nn", "hip_gemm_f32_nn_64x64",
+                                        "ada_gemm_k64_warp32_async_f32"};
+    const size_t eb = dtype_bytes(dtype);
+    void *a = NULL, *b = NULL, *c = NULL;
+    hipStream_t s = NULL;
+    hipEvent_t e0 = NULL, e1 = NULL;
+    int devices = 0;
+    char best[PYC_KERNEL_SYMBOL_MAX] = "";
+    double best_ms = 0.0;
+    int n = 0;
+    size_t i;
+    if ((dtype != PYC_DTYPE_F32 && dtype != PYC_DTYPE_BF16 && dtype != PYC_DTYPE_F16) || M <= 0 || N <= 0 ||
+        K <= 0 || iters <= 0 || !syms || sym_stride == 0 || !ms || cap <= 0) {
+        return -1;
+    }
+    if (env_true("PYC_CUDA_DISABLE") || hipGetDeviceCount(&devices) != hipSuccess || devices <= 0) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    pyc_mutex_lock(&g_dispatch_lock);
+    if (hipMalloc(&a, (size_t)M * K * eb) != hipSuccess || hipMalloc(&b, (size_t)K * N * eb) != hipSuccess ||
+        hipMalloc(&c, (size_t)M * N * eb) != hipSuccess || hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess ||
+        hipMemsetAsync(a, 0x3c, (size_t)M * K * eb, s) != hipSuccess ||
+        hipMemsetAsync(b, 0x3c, (size_t)K * N * eb, s) != hipSuccess) {
+        goto done;
+    }
+    for (i = 0; i < sizeof(cands) / sizeof(cands[0]) && n < cap; ++i) {
+        float t = 0.0f;
+        int it, ok = 1;
+        const int want = dtype == PYC_DTYPE_BF16 ? strstr(cands[i], "bf16") != NULL
+                         : dtype == PYC_DTYPE_F16 ? strstr(cands[i], "f16") != NULL && !strstr(cands[i], "bf16")
+                                                  : strstr(cands[i], "f32") != NULL;
+        if (!want || pyc_hip_gemm_dispatch(cands[i], M, N, K, a, b, c, 1.0f, 0.0f, NULL, 0, s) != 0) {
+            continue; /* other dtype, or the shape is outside the variant's preconditions */
+        }
+        ok = hipEventRecord(e0, s) == hipSuccess;
+        for (it = 0; ok && it < iters; ++it) {
+            ok = pyc_hip_gemm_dispatch(cands[i], M, N, K, a, b, c, 1.0f, 0.0f, NULL, 0, s) == 0;
+        }
+        ok = ok && hipEventRecord(e1, s) == hipSuccess && hipEventSynchronize(e1) == hipSuccess &&
+             hipEventElapsedTime(&t, e0, e1) == hipSuccess;
+        if (!ok) {
+            continue;
+        }
+        set_reason(syms + (size_t)n * sym_stride, sym_stride, cands[i]);
+        ms[n] = (double)t / iters;
+        if (best[0] == '\0' || ms[n] < best_ms) {
+            best_ms = ms[n];
+            set_reason(best, sizeof(best), cands[i]);
+        }
+        ++n;
+    }
+    if (best[0] != '\0') {
+        int slot = g_tuned_count;
+        int j;
+        for (j = 0; j < g_tuned_count; ++j) {
+            if (g_tuned[j].dtype == dtype && g_tuned[j].m == M && g_tuned[j].n == N && g_tuned[j].k == K) {
+                slot = j;
+            }
+        }
+        if (slot == TUNED_MAX) {
+            slot = TUNED_MAX - 1; /* table full: the newest shape replaces the last slot */
+        } else if (slot == g_tuned_count) {
+            g_tuned_count++;
+        }
+        g_tuned[slot].dtype = dtype;
+        g_tuned[slot].m = M;
+        g_tuned[slot].n = N;
+        g_tuned[slot].k = K;
+        set_reason(g_tuned[slot].symbol, sizeof(g_tuned[slot].symbol), best);
+        g_tune_gen++;
+    }
+done:
+    if (s) {
+        (void)hipStreamSynchronize(s);
+    }
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (s) (void)hipStreamDestroy(s);
+    if (a) (void)hipFree(a);
+    if (b) (void)hipFree(b);
+    if (c) (void)hipFree(c);
+    (void)hipGetLastError();
+    pyc_mutex_unlock(&g_dispatch_lock);
+    return n;
+}
+
 void pyc_hip_backend_release(void) {
     pyc_mutex_lock(&g_dispatch_lock);
     ws_release();

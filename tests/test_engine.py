@@ -557,3 +557,19 @@ def test_engine_wrapper_cpu_backend():
         assert key in j, key
     assert set(j["latency_ms"]) == {"mean", "p50", "p95", "min", "max"}
     assert j["execution_path"].startswith("cpu"), j["execution_path"]
+
+
+def test_hip_autotune_without_gpu():
+    """pyc_hip_autotune_gemm times nothing without a GPU (returns 0) and rejects
+    bad arguments; the engine's per-run autotune record stays in force then."""
+    import pyc_amd
+    L = pyc_amd.lib()
+    f = L.pyc_hip_autotune_gemm
+    f.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_char_p, C.c_size_t, C.POINTER(C.c_double), C.c_int]
+    f.restype = C.c_int
+    syms, ms = C.create_string_buffer(64 * 4), (C.c_double * 4)()
+    assert f(abi.DTYPE_BF16, 0, 8, 8, 1, syms, 64, ms, 4) == -1
+    assert f(abi.DTYPE_I32, 8, 8, 8, 1, syms, 64, ms, 4) == -1
+    import torch
+    if not torch.cuda.is_available():
+        assert f(abi.DTYPE_BF16, 8, 8, 8, 1, syms, 64, ms, 4) == 0
