@@ -109,8 +109,21 @@ int pyc_hip_w8a16_chain_reserve(int M, int nsteps, const int* N, const int* K);
 
 /* 1 if a chain launch on the current device gave up waiting for another
  * workgroup (its output is then invalid), 0 if not, -2 on a HIP error.
- * Synchronizes the device; clear != 0 resets the flag. */
+ * Synchronizes the device; clear != 0 resets the flag. pyc_run_model reads
+ * the flag after every run that launched a chain and turns a set flag into a
+ * native failure (reason "hip_chain_wait_timeout"). */
 int pyc_hip_w8a16_chain_error(int clear);
+
+/* 1 when pyc_hip_w8a16_chain_dispatch takes a chain of this shape (the
+ * preconditions above plus the kernel's unit and split-K slot limits), 0
+ * otherwise. Host only; the backend fuses fp8 steps into a chain launch only
+ * while this holds. */
+int pyc_hip_w8a16_chain_supported(int M, int nsteps, const int* N, const int* K);
+
+/* Sets the current device's chain timeout flag as a wait that ran out would,
+ * for tests of the failure handling (no kernel has to time out). 0, or -2 on
+ * a HIP error. */
+int pyc_hip_w8a16_chain_error_raise(void);
 
 /* GELU, exact erf form: y = 0.5 x (1 + erf(x / sqrt(2))), elementwise over n
  * elements (no reference kernel: the reference reports PYC_IR_OP_GELU as a

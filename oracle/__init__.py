@@ -53,6 +53,7 @@ def lib() -> ctypes.CDLL:
         L.orc_attention_f32.argtypes = [P, P, P, P, I, I, I, I, I, F, I, I]
         L.orc_conv2d_nhwc_f32.argtypes = [P, P, P, P] + [I] * 14
         L.orc_w8a16_layer.argtypes = [P, P, P, P, I, I, I, I]
+        L.orc_w8a16_layer_mt.argtypes = [P, P, P, P, I, I, I, I, I]
         L.orc_quantize_e4m3_per_col.argtypes = [P, I, I, P, P]
         _lib = L
     return _lib
@@ -164,14 +165,19 @@ def conv2d_nhwc_f32(x, w, bias, pad, stride, relu: bool, images=None) -> np.ndar
     return y
 
 
-def w8a16_layer(x_bits, wq, scale, relu: bool) -> np.ndarray:
+def w8a16_layer(x_bits, wq, scale, relu: bool, threads: int = 1) -> np.ndarray:
+    """Output channels split over `threads` threads; the result does not
+    depend on the thread count."""
     x_bits = np.ascontiguousarray(x_bits, dtype=np.uint16)
     wq = np.ascontiguousarray(wq, dtype=np.uint8)
     scale = np.ascontiguousarray(scale, dtype=np.float32)
     M, K = x_bits.shape
     N = wq.shape[0]
     y = np.empty((M, N), dtype=np.uint16)
-    lib().orc_w8a16_layer(_p(x_bits), _p(wq), _p(scale), _p(y), M, N, K, int(relu))
+    if threads > 1:
+        lib().orc_w8a16_layer_mt(_p(x_bits), _p(wq), _p(scale), _p(y), M, N, K, int(relu), int(threads))
+    else:
+        lib().orc_w8a16_layer(_p(x_bits), _p(wq), _p(scale), _p(y), M, N, K, int(relu))
     return y
 
 
@@ -184,12 +190,12 @@ def quantize_e4m3_per_col(w: np.ndarray):
     return wq, scale
 
 
-def w8a16_chain(x_bits, layers) -> np.ndarray:
+def w8a16_chain(x_bits, layers, threads: int = 1) -> np.ndarray:
     """layers: list of (wq_up [F,D], s_up [F], wq_down [D,F], s_down [D])."""
     h = x_bits
     for wq_up, s_up, wq_dn, s_dn in layers:
-        t = w8a16_layer(h, wq_up, s_up, True)
-        h = w8a16_layer(t, wq_dn, s_dn, False)
+        t = w8a16_layer(h, wq_up, s_up, True, threads)
+        h = w8a16_layer(t, wq_dn, s_dn, False, threads)
     return h
 
 

@@ -389,12 +389,47 @@ void orc_conv2d_nhwc_f32(const float* x, const float* w, const float* bias, floa
 /* ---------------------------------------------------------------- fp8 decode layer */
 
 /* One weight-only fp8 layer: Y[m,n] = bf16( relu?( scale[n] * sum_k X[m,k] * e4m3(Wq[n,k]) ) ),
- * X bf16 [M,K], Wq [N,K] e4m3fn, Y bf16 [M,N]. Sum in fp32, k ascending. */
-void orc_w8a16_layer(const uint16_t* x, const uint8_t* wq, const float* scale,
-                     uint16_t* y, int M, int N, int K, int relu) {
+ * X bf16 [M,K], Wq [N,K] e4m3fn, Y bf16 [M,N]. Sum in fp32, k ascending.
+ * orc_w8a16_layer_mt splits the output channels over `threads` threads (each
+ * channel's arithmetic is the same as with one). */
+typedef struct {
+    const float* xf;
+    const uint8_t* wq;
+    const float* scale;
+    const float* lut;
+    uint16_t* y;
+    int M, N, K, relu, n0, n1;
+} orc_w8_job;
+
+static void* orc_w8_cols(void* arg) {
+    const orc_w8_job* j = (const orc_w8_job*)arg;
+    int m, n, kk;
+    for (n = j->n0; n < j->n1; ++n) {
+        const uint8_t* wr = j->wq + (size_t)n * j->K;
+        for (m = 0; m < j->M; ++m) {
+            const float* xr = j->xf + (size_t)m * j->K;
+            float acc = 0.0f;
+            for (kk = 0; kk < j->K; ++kk) {
+                acc += xr[kk] * j->lut[wr[kk]];
+            }
+            acc *= j->scale[n];
+            if (j->relu && acc < 0.0f) {
+                acc = 0.0f;
+            }
+            j->y[(size_t)m * j->N + n] = orc_f32_to_bf16(acc);
+        }
+    }
+    return NULL;
+}
+
+void orc_w8a16_layer_mt(const uint16_t* x, const uint8_t* wq, const float* scale,
+                        uint16_t* y, int M, int N, int K, int relu, int threads) {
     float lut[256];
     float* xf = (float*)malloc((size_t)M * K * sizeof(float));
-    int i, m, n, kk;
+    orc_w8_job jobs[64];
+    pthread_t tid[64];
+    int started[64];
+    int i, t, per;
     if (!xf) {
         return;
     }
@@ -404,22 +439,30 @@ void orc_w8a16_layer(const uint16_t* x, const uint8_t* wq, const float* scale,
     for (i = 0; i < M * K; ++i) {
         xf[i] = orc_bf16_to_f32(x[i]);
     }
-    for (n = 0; n < N; ++n) {
-        const uint8_t* wr = wq + (size_t)n * K;
-        for (m = 0; m < M; ++m) {
-            const float* xr = xf + (size_t)m * K;
-            float acc = 0.0f;
-            for (kk = 0; kk < K; ++kk) {
-                acc += xr[kk] * lut[wr[kk]];
-            }
-            acc *= scale[n];
-            if (relu && acc < 0.0f) {
-                acc = 0.0f;
-            }
-            y[(size_t)m * N + n] = orc_f32_to_bf16(acc);
+    if (threads < 1) threads = 1;
+    if (threads > 64) threads = 64;
+    if (threads > N) threads = N;
+    per = (N + threads - 1) / threads;
+    for (t = 0; t < threads; ++t) {
+        orc_w8_job jb = {xf, wq, scale, lut, y, M, N, K, relu, t * per < N ? t * per : N,
+                         (t + 1) * per < N ? (t + 1) * per : N};
+        jobs[t] = jb;
+        started[t] = threads > 1 && pthread_create(&tid[t], NULL, orc_w8_cols, &jobs[t]) == 0;
+        if (!started[t]) {
+            orc_w8_cols(&jobs[t]);
+        }
+    }
+    for (t = 0; t < threads; ++t) {
+        if (started[t]) {
+            pthread_join(tid[t], NULL);
         }
     }
     free(xf);
+}
+
+void orc_w8a16_layer(const uint16_t* x, const uint8_t* wq, const float* scale,
+                     uint16_t* y, int M, int N, int K, int relu) {
+    orc_w8a16_layer_mt(x, wq, scale, y, M, N, K, relu, 1);
 }
 
 /* Per-output-channel quantization of a weight W[K,N] (row-major, as the

@@ -47,6 +47,10 @@ def _declare(L: C.CDLL) -> None:
     L.pyc_hip_w8a16_chain_reserve.restype = I
     L.pyc_hip_w8a16_chain_error.argtypes = [I]
     L.pyc_hip_w8a16_chain_error.restype = I
+    L.pyc_hip_w8a16_chain_supported.argtypes = [I, I, P, P]
+    L.pyc_hip_w8a16_chain_supported.restype = I
+    L.pyc_hip_w8a16_chain_error_raise.argtypes = []
+    L.pyc_hip_w8a16_chain_error_raise.restype = I
     L.pyc_hip_gelu_dispatch.argtypes = [S, Z, P, P, P]
     L.pyc_hip_gelu_dispatch.restype = I
     L.pyc_hip_layernorm_dispatch.argtypes = [S, I, I, F, P, P, P, P, P]

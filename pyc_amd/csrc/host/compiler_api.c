@@ -38,6 +38,7 @@
 #include <time.h>
 #include <unistd.h>
 
+#include "cpu_ops.h"
 #include "pyc/cuda_backend.h"
 #include "pyc/hip_backend.h"
 #include "pyc/kernel_registry.h"
@@ -1082,45 +1083,113 @@ static void cpu_gemm(const float* a, const float* b, float* c, size_t m, size_t 
     }
 }
 
-/* The engine's CPU executor: F32 INPUT/MATMUL/ADD/RELU/OUTPUT (reference
- * compiler_api.c:1877-2092), with ADD broadcasting a [N] or [1] operand. */
+/* Result type of a computed value: half when either operand is half (an fp32
+ * bias added to a bf16 GEMM result stays bf16, as the device stores it). */
+static pyc_dtype join_dtype(pyc_dtype a, pyc_dtype b) {
+    return a == PYC_DTYPE_F32 && (b == PYC_DTYPE_BF16 || b == PYC_DTYPE_F16) ? b : a;
+}
+
+static int float_dtype(pyc_dtype t) {
+    return t == PYC_DTYPE_F32 || t == PYC_DTYPE_BF16 || t == PYC_DTYPE_F16;
+}
+
+/* The engine's CPU executor (reference compiler_api.c:1877-2092), the
+ * fallback of pyc_cuda_dispatch. Every value is held as fp32; values of a
+ * half type are decoded on input and rounded to their type after every op,
+ * as the device stores them, and encoded on output.
+ *   - F32 INPUT/MATMUL/ADD/RELU/OUTPUT follow the reference exactly (GEMM
+ *     order and threading of compiler_api.c:1747-1875); ADD broadcasts a [N]
+ *     or [1] operand;
+ *   - beyond the reference (which fails on them): bf16/f16 values, the
+ *     weight-only fp8 MATMUL (rhs e4m3 stored [N,K], third input fp32
+ *     scale[N]), CONV2D (NHWC x, KRSC w), ATTENTION ([B,H,S,D], scale
+ *     1/sqrt(D)), GELU and LAYERNORM (cpu_ops.c), with the op-name attribute
+ *     conventions the GPU backend reads. CONST and REDUCE_SUM still fail. */
 static int execute_cpu_graph(const pyc_ir_module* m, const pyc_tensor* inputs, size_t n_in, pyc_tensor* outputs,
                              size_t n_out, void* ctx) {
     pyc_compiled_model* model = (pyc_compiled_model*)ctx;
     const float** val = (const float**)calloc(m->op_count, sizeof(float*));
     float** owned = (float**)calloc(m->op_count, sizeof(float*));
     size_t* count = (size_t*)calloc(m->op_count, sizeof(size_t));
+    pyc_shape* shp = (pyc_shape*)calloc(m->op_count, sizeof(pyc_shape));
+    pyc_dtype* vt = (pyc_dtype*)calloc(m->op_count, sizeof(pyc_dtype));
+    const uint8_t** raw = (const uint8_t**)calloc(m->op_count, sizeof(uint8_t*));
     size_t i, ii = 0, oi = 0;
     int fail = 0;
-    if (!val || !owned || !count) {
-        free(val);
-        free(owned);
-        free(count);
-        return -1;
+    if (!val || !owned || !count || !shp || !vt || !raw) {
+        fail = 1;
     }
     for (i = 0; i < m->op_count && !fail; ++i) {
         const pyc_ir_op* op = &m->ops[i];
         const int a = op->input_count > 0 ? op->input_ids[0] : -1;
         const int b = op->input_count > 1 ? op->input_ids[1] : -1;
+        const int c3 = op->input_count > 2 ? op->input_ids[2] : -1;
         float* out = NULL;
         size_t need = 0;
+        int conv[11] = {0};
+        if ((a >= (int)i) || (b >= (int)i) || (c3 >= (int)i)) {
+            fail = 1;
+            break;
+        }
         switch (op->kind) {
-            case PYC_IR_OP_INPUT:
+            case PYC_IR_OP_INPUT: {
+                const pyc_dtype t = op->dtype;
                 count[i] = shape_elems(&op->shape);
-                if (ii >= n_in || !inputs[ii].data || inputs[ii].dtype != PYC_DTYPE_F32 || count[i] == 0 ||
-                    inputs[ii].size_bytes < count[i] * sizeof(float)) {
+                shp[i] = op->shape;
+                vt[i] = t;
+                if (ii >= n_in || !inputs[ii].data || inputs[ii].dtype != t || count[i] == 0 ||
+                    inputs[ii].size_bytes < count[i] * dtype_bytes(t) || dtype_bytes(t) == 0) {
                     fail = 1;
                     break;
                 }
-                val[i] = (const float*)inputs[ii++].data;
+                if (t == PYC_DTYPE_F32) {
+                    val[i] = (const float*)inputs[ii].data;
+                } else if (t == PYC_DTYPE_BF16 || t == PYC_DTYPE_F16) {
+                    const uint16_t* h = (const uint16_t*)inputs[ii].data;
+                    size_t j;
+                    owned[i] = (float*)malloc(count[i] * sizeof(float));
+                    if (!owned[i]) {
+                        fail = 1;
+                        break;
+                    }
+                    for (j = 0; j < count[i]; ++j) {
+                        owned[i][j] = t == PYC_DTYPE_BF16 ? pyc_cpu_bf16_to_f32(h[j]) : pyc_cpu_f16_to_f32(h[j]);
+                    }
+                    val[i] = owned[i];
+                } else if (t == PYC_DTYPE_FP8_E4M3) {
+                    raw[i] = (const uint8_t*)inputs[ii].data; /* an fp8 MATMUL's weight, read as codes */
+                } else {
+                    fail = 1;
+                    break;
+                }
+                ii++;
                 continue;
+            }
             case PYC_IR_OP_MATMUL:
-                if (a < 0 || b < 0 || !val[a] || !val[b] || m->ops[a].shape.rank != 2 || m->ops[b].shape.rank != 2 ||
-                    m->ops[a].shape.dims[1] != m->ops[b].shape.dims[0]) {
+                if (a < 0 || b < 0 || !val[a] || shp[a].rank != 2 || shp[b].rank != 2) {
                     fail = 1;
                     break;
                 }
-                count[i] = (size_t)m->ops[a].shape.dims[0] * (size_t)m->ops[b].shape.dims[1];
+                if (vt[b] == PYC_DTYPE_FP8_E4M3) {
+                    /* X [M,K] bf16, Wq [N,K] e4m3, scale [N] fp32 -> bf16 [M,N] */
+                    if (!raw[b] || c3 < 0 || !val[c3] || vt[c3] != PYC_DTYPE_F32 || vt[a] != PYC_DTYPE_BF16 ||
+                        shp[b].dims[1] != shp[a].dims[1] || count[c3] != (size_t)shp[b].dims[0]) {
+                        fail = 1;
+                        break;
+                    }
+                    vt[i] = PYC_DTYPE_BF16;
+                    shp[i].dims[1] = shp[b].dims[0];
+                } else {
+                    if (!val[b] || shp[a].dims[1] != shp[b].dims[0] || vt[a] != vt[b] || !float_dtype(vt[a])) {
+                        fail = 1;
+                        break;
+                    }
+                    vt[i] = vt[a];
+                    shp[i].dims[1] = shp[b].dims[1];
+                }
+                shp[i].rank = 2;
+                shp[i].dims[0] = shp[a].dims[0];
+                count[i] = (size_t)shp[i].dims[0] * (size_t)shp[i].dims[1];
                 break;
             case PYC_IR_OP_ADD:
                 if (a < 0 || b < 0 || !val[a] || !val[b] || count[b] == 0 || count[a] % count[b] != 0) {
@@ -1128,24 +1197,100 @@ static int execute_cpu_graph(const pyc_ir_module* m, const pyc_tensor* inputs, s
                     break;
                 }
                 count[i] = count[a];
+                shp[i] = shp[a];
+                vt[i] = join_dtype(vt[a], vt[b]);
                 break;
             case PYC_IR_OP_RELU:
-                if (a < 0 || !val[a]) {
+            case PYC_IR_OP_GELU:
+                if (a < 0 || !val[a] || (op->kind == PYC_IR_OP_GELU && op->input_count != 1)) {
                     fail = 1;
                     break;
                 }
                 count[i] = count[a];
+                shp[i] = shp[a];
+                vt[i] = vt[a];
                 break;
-            case PYC_IR_OP_OUTPUT:
-                if (a < 0 || !val[a] || oi >= n_out || !outputs[oi].data ||
-                    outputs[oi].size_bytes < count[a] * sizeof(float)) {
+            case PYC_IR_OP_LAYERNORM: {
+                size_t k;
+                if (a < 0 || !val[a] || shp[a].rank < 1 || op->input_count > 3 || !(pyc_op_eps(op->name) >= 0.0f)) {
                     fail = 1;
                     break;
                 }
-                memcpy(outputs[oi++].data, val[a], count[a] * sizeof(float));
+                for (k = 1; k < op->input_count; ++k) {
+                    const int gb = op->input_ids[k];
+                    if (gb < 0 || !val[gb] || count[gb] != (size_t)shp[a].dims[shp[a].rank - 1]) {
+                        fail = 1;
+                    }
+                }
+                count[i] = count[a];
+                shp[i] = shp[a];
+                vt[i] = vt[a];
+                break;
+            }
+            case PYC_IR_OP_CONV2D: {
+                int sh, sw, ph, pw;
+                if (a < 0 || b < 0 || !val[a] || !val[b] || shp[a].rank != 4 || shp[b].rank != 4 ||
+                    shp[a].dims[3] != shp[b].dims[3] || vt[a] != vt[b] || !float_dtype(vt[a])) {
+                    fail = 1;
+                    break;
+                }
+                pyc_op_conv_attrs(op->name, &sh, &sw, &ph, &pw);
+                conv[0] = (int)shp[a].dims[0];
+                conv[1] = (int)shp[a].dims[1];
+                conv[2] = (int)shp[a].dims[2];
+                conv[3] = (int)shp[a].dims[3];
+                conv[4] = (int)shp[b].dims[0];
+                conv[5] = (int)shp[b].dims[1];
+                conv[6] = (int)shp[b].dims[2];
+                conv[7] = ph;
+                conv[8] = pw;
+                conv[9] = sh;
+                conv[10] = sw;
+                if (sh <= 0 || sw <= 0 || ph < 0 || pw < 0 || conv[1] + 2 * ph < conv[5] || conv[2] + 2 * pw < conv[6]) {
+                    fail = 1;
+                    break;
+                }
+                shp[i].rank = 4;
+                shp[i].dims[0] = conv[0];
+                shp[i].dims[1] = (conv[1] + 2 * ph - conv[5]) / sh + 1;
+                shp[i].dims[2] = (conv[2] + 2 * pw - conv[6]) / sw + 1;
+                shp[i].dims[3] = conv[4];
+                count[i] = shape_elems(&shp[i]);
+                vt[i] = vt[a];
+                break;
+            }
+            case PYC_IR_OP_ATTENTION:
+                if (a < 0 || b < 0 || c3 < 0 || !val[a] || !val[b] || !val[c3] || shp[a].rank != 4 ||
+                    memcmp(&shp[a], &shp[b], sizeof(pyc_shape)) != 0 || memcmp(&shp[a], &shp[c3], sizeof(pyc_shape)) != 0 ||
+                    vt[a] != vt[b] || vt[a] != vt[c3] || !float_dtype(vt[a])) {
+                    fail = 1;
+                    break;
+                }
+                count[i] = count[a];
+                shp[i] = shp[a];
+                vt[i] = vt[a];
+                break;
+            case PYC_IR_OP_OUTPUT: {
+                const pyc_dtype ot = oi < n_out ? outputs[oi].dtype : PYC_DTYPE_UNKNOWN;
+                size_t j;
+                if (a < 0 || !val[a] || oi >= n_out || !outputs[oi].data || !float_dtype(ot) ||
+                    outputs[oi].size_bytes < count[a] * dtype_bytes(ot)) {
+                    fail = 1;
+                    break;
+                }
+                if (ot == PYC_DTYPE_F32) {
+                    memcpy(outputs[oi].data, val[a], count[a] * sizeof(float));
+                } else {
+                    uint16_t* h = (uint16_t*)outputs[oi].data;
+                    for (j = 0; j < count[a]; ++j) {
+                        h[j] = ot == PYC_DTYPE_BF16 ? pyc_cpu_f32_to_bf16(val[a][j]) : pyc_cpu_f32_to_f16(val[a][j]);
+                    }
+                }
+                oi++;
                 continue;
+            }
             default:
-                fail = 1; /* CONST / GELU / REDUCE_SUM / LAYERNORM / CONV2D / ATTENTION */
+                fail = 1; /* CONST / REDUCE_SUM */
                 break;
         }
         if (fail) {
@@ -1161,29 +1306,70 @@ static int execute_cpu_graph(const pyc_ir_module* m, const pyc_tensor* inputs, s
                 break;
             }
         }
-        if (op->kind == PYC_IR_OP_MATMUL) {
-            cpu_gemm(val[a], val[b], out, (size_t)m->ops[a].shape.dims[0], (size_t)m->ops[a].shape.dims[1],
-                     (size_t)m->ops[b].shape.dims[1]);
-        } else if (op->kind == PYC_IR_OP_ADD) {
-            size_t j;
-            const size_t nb = count[b];
-            for (j = 0; j < count[i]; ++j) {
-                out[j] = val[a][j] + val[b][j % nb];
+        switch (op->kind) {
+            case PYC_IR_OP_MATMUL:
+                if (vt[b] == PYC_DTYPE_FP8_E4M3) {
+                    pyc_cpu_w8a16_gemm(val[a], raw[b], val[c3], out, (int)shp[a].dims[0], (int)shp[b].dims[0],
+                                       (int)shp[a].dims[1]);
+                } else {
+                    cpu_gemm(val[a], val[b], out, (size_t)shp[a].dims[0], (size_t)shp[a].dims[1],
+                             (size_t)shp[b].dims[1]);
+                }
+                break;
+            case PYC_IR_OP_ADD: {
+                size_t j;
+                const size_t nb = count[b];
+                for (j = 0; j < count[i]; ++j) {
+                    out[j] = val[a][j] + val[b][j % nb];
+                }
+                break;
             }
-        } else {
+            case PYC_IR_OP_RELU: {
+                size_t j;
+                for (j = 0; j < count[i]; ++j) {
+                    out[j] = val[a][j] > 0.0f ? val[a][j] : 0.0f;
+                }
+                break;
+            }
+            case PYC_IR_OP_GELU:
+                pyc_cpu_gelu(val[a], out, count[i]);
+                break;
+            case PYC_IR_OP_LAYERNORM: {
+                const size_t D = (size_t)shp[a].dims[shp[a].rank - 1];
+                pyc_cpu_layernorm(val[a], op->input_count > 1 ? val[op->input_ids[1]] : NULL,
+                                  op->input_count > 2 ? val[op->input_ids[2]] : NULL, out, count[i] / D, D,
+                                  pyc_op_eps(op->name));
+                break;
+            }
+            case PYC_IR_OP_CONV2D:
+                pyc_cpu_conv2d_nhwc(val[a], val[b], out, conv[0], conv[1], conv[2], conv[3], conv[4], conv[5],
+                                    conv[6], conv[7], conv[8], conv[9], conv[10]);
+                break;
+            case PYC_IR_OP_ATTENTION:
+                pyc_cpu_attention(val[a], val[b], val[c3], out, (int)shp[a].dims[0], (int)shp[a].dims[1],
+                                  (int)shp[a].dims[2], (int)shp[a].dims[3], pyc_op_is_causal(op->name),
+                                  1.0f / sqrtf((float)shp[a].dims[3]));
+                break;
+            default:
+                break;
+        }
+        if (vt[i] != PYC_DTYPE_F32) {
             size_t j;
             for (j = 0; j < count[i]; ++j) {
-                out[j] = val[a][j] > 0.0f ? val[a][j] : 0.0f;
+                out[j] = pyc_cpu_round_to(vt[i], out[j]);
             }
         }
         val[i] = out;
     }
-    for (i = 0; i < m->op_count; ++i) {
+    for (i = 0; owned && i < m->op_count; ++i) {
         free(owned[i]);
     }
     free(val);
     free(owned);
     free(count);
+    free(shp);
+    free(vt);
+    free(raw);
     return fail ? -1 : 0;
 }
 

@@ -53,10 +53,16 @@
 #include "pyc/cuda_backend.h"
 #include "pyc/hip_backend.h"
 #include "pyc/kernel_registry.h"
+#include "cpu_ops.h"
 #include "pyc_mutex.h"
 
 /* split-K workspace of the fp8 GEMM (gemm_w8a16.hip); allocates outside capture */
 int pyc_hip_w8a16_reserve(int N, int K);
+/* chain kernel preconditions and its timeout word (gemm_w8a16.hip) */
+int pyc_hip_w8a16_chain_supported(int M, int nsteps, const int* N, const int* K);
+int pyc_hip_w8a16_chain_error_enqueue(int* host_dst, void* stream);
+/* 1 when a GEMM symbol takes alpha = 1, beta = 0 only (hip_kernels.c) */
+int pyc_hip_gemm_symbol_unit_epilogue_only(const char* symbol);
 
 static pyc_mutex g_dispatch_lock = PYC_MUTEX_INIT;
 
@@ -268,25 +274,48 @@ static int value_private(const hip_plan* p, int v, size_t reader) {
 
 /* Number of consecutive fp8-weight steps from step s that run as one chain
  * launch (pyc_hip_w8a16_chain_dispatch): each reads the previous one's output,
- * which nothing else reads, with K % 128 == 0 and N % 64 == 0 throughout.
- * 1 when step s starts no chain. */
+ * which nothing else reads, and the chain so far meets the chain kernel's
+ * preconditions (pyc_hip_w8a16_chain_supported: K % 128 == 0 and N % 64 == 0
+ * for every step, unit and split-K slot limits). 1 when step s starts no
+ * chain; those steps run one launch each on the per-layer kernel. */
 #define HIP_CHAIN_MAX_STEPS 32
 static size_t w8_chain_len(const hip_plan* p, size_t s) {
     size_t e = s;
+    int cn[HIP_CHAIN_MAX_STEPS], ck[HIP_CHAIN_MAX_STEPS];
     const hip_step* a = &p->steps[s];
-    if (a->kind != ST_W8A16 || a->add_mode != ADD_NONE || (a->k % 128) != 0 || (a->n % 64) != 0) {
+    if (a->kind != ST_W8A16 || a->add_mode != ADD_NONE) {
         return 1;
     }
+    cn[0] = a->n;
+    ck[0] = a->k;
     while (e + 1 < p->nsteps && e + 1 - s < HIP_CHAIN_MAX_STEPS) {
         const hip_step* cur = &p->steps[e];
         const hip_step* nx = &p->steps[e + 1];
+        const size_t len = e + 2 - s;
         if (nx->kind != ST_W8A16 || nx->add_mode != ADD_NONE || nx->in[0] != cur->out || nx->m != cur->m ||
-            nx->k != cur->n || (nx->n % 64) != 0 || !value_private(p, cur->out, e + 1)) {
+            nx->k != cur->n || !value_private(p, cur->out, e + 1)) {
+            break;
+        }
+        cn[len - 1] = nx->n;
+        ck[len - 1] = nx->k;
+        if (!pyc_hip_w8a16_chain_supported(a->m, (int)len, cn, ck)) {
             break;
         }
         ++e;
     }
     return e - s + 1;
+}
+
+/* 1 when the plan launches the chain kernel somewhere. */
+static int plan_has_chain(const hip_plan* p) {
+    size_t s;
+    for (s = 0; s < p->nsteps; ++s) {
+        const size_t clen = w8_chain_len(p, s);
+        if (clen >= 2) {
+            return 1;
+        }
+    }
+    return 0;
 }
 
 static int consumers(const pyc_ir_module* m, int id, int* only) {
@@ -307,22 +336,6 @@ static int consumers(const pyc_ir_module* m, int id, int* only) {
 
 static int valid_id(const pyc_ir_module* m, int id) {
     return id >= 0 && (size_t)id < m->op_count;
-}
-
-/* conv attributes from the op name suffix "@s<sh>x<sw>p<ph>x<pw>" */
-static void conv_attrs(const char* name, int* sh, int* sw, int* ph, int* pw) {
-    const char* at = strchr(name, '@');
-    *sh = *sw = 1;
-    *ph = *pw = 0;
-    if (at) {
-        int a, b, c, d;
-        if (sscanf(at, "@s%dx%dp%dx%d", &a, &b, &c, &d) == 4) {
-            *sh = a;
-            *sw = b;
-            *ph = c;
-            *pw = d;
-        }
-    }
 }
 
 static void set_value(hip_plan* plan, int id, const pyc_shape* shape, pyc_dtype t) {
@@ -501,6 +514,12 @@ static int build_plan(const pyc_ir_module* m, hip_plan* plan) {
                 if (st->kind == ST_W8A16 && st->add_mode != ADD_NONE) {
                     return 1; /* the fp8 epilogue is scale (+ReLU) only */
                 }
+                if (st->kind == ST_GEMM && st->add_mode == ADD_MATRIX &&
+                    pyc_hip_gemm_symbol_unit_epilogue_only(st->symbol)) {
+                    /* a matrix addend runs as beta = 1, which a tuned or
+                     * promoted unit-epilogue variant does not take */
+                    set_reason(st->symbol, sizeof(st->symbol), default_gemm_symbol(st->dtype));
+                }
                 plan->nsteps++;
                 break;
             }
@@ -525,7 +544,7 @@ static int build_plan(const pyc_ir_module* m, hip_plan* plan) {
                     plan->vdtype[w] != plan->vdtype[x]) {
                     return 1;
                 }
-                conv_attrs(op->name, &sh, &sw, &ph, &pw);
+                pyc_op_conv_attrs(op->name, &sh, &sw, &ph, &pw);
                 memset(st, 0, sizeof(*st));
                 st->kind = ST_CONV;
                 st->dtype = plan->vdtype[x];
@@ -603,7 +622,7 @@ static int build_plan(const pyc_ir_module* m, hip_plan* plan) {
                 st->attn[1] = (int)qs->dims[1];
                 st->attn[2] = (int)qs->dims[2];
                 st->attn[3] = (int)qs->dims[3];
-                st->attn[4] = strstr(op->name, "causal") != NULL;
+                st->attn[4] = pyc_op_is_causal(op->name);
                 if (st->attn[3] != 64 && st->attn[3] != 128) {
                     return 1;
                 }
@@ -642,7 +661,6 @@ static int build_plan(const pyc_ir_module* m, hip_plan* plan) {
                 st->elems = shape_elems(&plan->vshape[x]);
                 if (is_ln) {
                     const pyc_shape* xs = &plan->vshape[x];
-                    const char* e = strstr(op->name, "@eps");
                     if (xs->rank < 1 || xs->dims[xs->rank - 1] <= 0 || xs->dims[xs->rank - 1] > 0x7FFFFFFF) {
                         return 1;
                     }
@@ -651,7 +669,7 @@ static int build_plan(const pyc_ir_module* m, hip_plan* plan) {
                         return 1;
                     }
                     st->m = (int)(st->elems / (size_t)st->n);
-                    st->eps = e ? strtof(e + 4, NULL) : 1e-5f;
+                    st->eps = pyc_op_eps(op->name);
                     if (!(st->eps >= 0.0f)) {
                         return 1;
                     }
@@ -718,6 +736,7 @@ static struct {
     const void* last_host[PYC_IR_MAX_OPS];
     size_t last_bytes[PYC_IR_MAX_OPS];
     int uploaded[PYC_IR_MAX_OPS];
+    int* chain_err;                /* pinned copy of the chain kernel's timeout word */
     /* graph replay */
     hipGraphExec_t gexec;
     hipGraph_t graph;
@@ -748,6 +767,9 @@ static void ws_release(void) {
             (void)hipHostFree(g_ws.stage_out[i].ptr);
         }
     }
+    if (g_ws.chain_err) {
+        (void)hipHostFree(g_ws.chain_err);
+    }
     if (g_ws.ready) {
         (void)hipEventDestroy(g_ws.ev0);
         (void)hipEventDestroy(g_ws.ev1);
@@ -770,6 +792,11 @@ static int ws_init(void) {
     if (hipEventCreate(&g_ws.ev0) != hipSuccess || hipEventCreate(&g_ws.ev1) != hipSuccess) {
         return -1;
     }
+    if (hipHostMalloc((void**)&g_ws.chain_err, 64, hipHostMallocDefault) != hipSuccess) {
+        g_ws.chain_err = NULL;
+        return -1;
+    }
+    *g_ws.chain_err = 0;
     g_ws.ready = 1;
     return 0;
 }
@@ -1006,6 +1033,7 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
     int dev_out[64];            /* output whose caller tensor is device memory */
     int out_d2d[64];            /* ... filled by a device-to-device copy (its value is stored elsewhere) */
     int any_dev = 0;
+    int has_chain = 0;
     size_t i;
     uint64_t sig = 1469598103934665603ull;
     int replayed = 0;
@@ -1019,6 +1047,7 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
     if (plan.n_outputs > output_count || plan.n_outputs > 64) {
         return 1;
     }
+    has_chain = plan_has_chain(&plan);
     if (ws_init() != 0) {
         snprintf(why, why_cap, "hip_workspace_init_failed");
         return -1;
@@ -1096,6 +1125,23 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
             return -1;
         }
     }
+    for (i = 0; i < m->op_count; ++i) {
+        any_dev |= dev_in[i];
+    }
+    for (i = 0; i < plan.n_outputs; ++i) {
+        any_dev |= dev_out[i];
+    }
+    if (any_dev) {
+        /* The caller's device tensors may come from work on any stream, and
+         * its outputs may still be in use there: neither the bias read-back
+         * below nor the backend's own stream orders against that work, so
+         * wait for the whole device before anything touches them. */
+        if (hipDeviceSynchronize() != hipSuccess) {
+            snprintf(why, why_cap, "hip_sync_failed");
+            return -1;
+        }
+    }
+
     /* fp32 add operands: uploaded as part of the inputs; converted copies for half ones */
     for (i = 0; i < plan.nsteps; ++i) {
         const hip_step* st = &plan.steps[i];
@@ -1161,17 +1207,17 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
     sig = fnv(sig, m->ops, m->op_count * sizeof(pyc_ir_op));
     sig = fnv(sig, &skip_out, sizeof(skip_out));
     sig = fnv(sig, &g_tune_gen, sizeof(g_tune_gen));
+    /* the planned kernels: an env or registry change of a symbol recaptures */
+    for (i = 0; i < plan.nsteps; ++i) {
+        const size_t clen = w8_chain_len(&plan, i);
+        sig = fnv(sig, plan.steps[i].symbol, strlen(plan.steps[i].symbol));
+        sig = fnv(sig, &clen, sizeof(clen));
+    }
     for (i = 0; i < m->op_count; ++i) {
         if (plan.input_ordinal[i] >= 0) {
             sig = fnv(sig, &copy_in[i], sizeof(int));
             sig = fnv(sig, &dev_in[i], sizeof(int));
         }
-    }
-    for (i = 0; i < m->op_count; ++i) {
-        any_dev |= dev_in[i];
-    }
-    for (i = 0; i < plan.n_outputs; ++i) {
-        any_dev |= dev_out[i];
     }
     /* a graph bakes in the caller's device tensors: their addresses are part of the run */
     sig = fnv(sig, vp, sizeof(vp));
@@ -1242,6 +1288,9 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
             if (rc == 0 && !use_graph) {
                 rc = hipEventRecord(g_ws.ev1, g_ws.stream) == hipSuccess ? 0 : -1;
             }
+            if (rc == 0 && has_chain && pyc_hip_w8a16_chain_error_enqueue(g_ws.chain_err, g_ws.stream) != 0) {
+                rc = -1; /* the chain's timeout word is read back with every run */
+            }
             for (i = 0; rc == 0 && i < plan.n_outputs; ++i) {
                 const int src = plan.output_src[i];
                 if (dev_out[i]) {
@@ -1284,14 +1333,6 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
     }
 
     t0 = now_ms();
-    if (any_dev) {
-        /* the caller's device tensors may come from work on any stream: the
-         * backend's own stream does not order against those, so wait for it */
-        if (hipDeviceSynchronize() != hipSuccess) {
-            snprintf(why, why_cap, "hip_sync_failed");
-            return -1;
-        }
-    }
     if (use_graph) {
         if (hipEventRecord(g_ws.ev0, g_ws.stream) != hipSuccess ||
             hipGraphLaunch(g_ws.gexec, g_ws.stream) != hipSuccess ||
@@ -1302,6 +1343,16 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
     }
     if (hipStreamSynchronize(g_ws.stream) != hipSuccess) {
         snprintf(why, why_cap, "hip_sync_failed");
+        return -1;
+    }
+    if (has_chain && *g_ws.chain_err != 0) {
+        /* A chain workgroup gave up waiting for another one (the grid was not
+         * all resident): the outputs are invalid. Clear the word and fail the
+         * run, so the native-failure contract applies (workspace release, CPU
+         * fallback, or an error for device tensors / strict mode). */
+        *g_ws.chain_err = 0;
+        (void)pyc_hip_w8a16_chain_error(1);
+        snprintf(why, why_cap, "hip_chain_wait_timeout");
         return -1;
     }
     if (trace) {
@@ -1641,9 +1692,11 @@ pyc_cuda_dispatch_status pyc_cuda_dispatch(const pyc_ir_module* module, const py
  * mean ms in syms/ms), 0 when nothing could be timed, -1 on bad arguments. */
 int pyc_hip_autotune_gemm(pyc_dtype dtype, int M, int N, int K, int iters, char* syms, size_t sym_stride,
                           double* ms, int cap) {
+    /* one entry per distinct kernel: the reference's fp32 alias
+     * ada_gemm_k64_warp32_async_f32 runs hip_gemm_f32_nn_64x64's kernel with a
+     * narrower epilogue, so timing it would only pick between equal launches */
     static const char* const cands[] = {"hip_gemm_bf16_nn_256x256", "hip_gemm_bf16_nn_128x128", "hip_gemm_bf16_nn",
-                                        "cutlass_gemm_tensorcore_bf16", "hip_gemm_f16_nn", "hip_gemm_f32_nn_64x64",
-                                        "ada_gemm_k64_warp32_async_f32"};
+                                        "cutlass_gemm_tensorcore_bf16", "hip_gemm_f16_nn", "hip_gemm_f32_nn_64x64"};
     const size_t eb = dtype_bytes(dtype);
     void *a = NULL, *b = NULL, *c = NULL;
     hipStream_t s = NULL;

@@ -119,6 +119,13 @@ static const hip_variant* find_variant(const char* symbol, int kind) {
     return NULL;
 }
 
+/* 1 when the GEMM symbol takes only alpha = 1 and beta = 0 (its epilogue
+ * cannot fold a matrix addend), 0 otherwise or for unknown symbols. */
+int pyc_hip_gemm_symbol_unit_epilogue_only(const char* symbol) {
+    const hip_variant* v = find_variant(symbol, VK_GEMM);
+    return v && v->unit_epilogue_only ? 1 : 0;
+}
+
 int pyc_hip_kernel_symbol_count(const char* op_key) {
     size_t i;
     int n = 0;

@@ -1030,22 +1030,31 @@ struct W8ChainWorkspace {
 W8ChainWorkspace g_chainws[kMaxDevices];
 
 constexpr int kChainMaxUnits = 4096;  // N <= 4096 * 64 per step
-// done[] (one 128-byte line per step), then the exit and error words
-constexpr size_t kChainCtlBytes = (size_t)(pyc::kChainMaxSteps + 2) * pyc::kChainPad * sizeof(int);
-constexpr size_t kChainHeadBytes = kChainCtlBytes + (size_t)pyc::kChainMaxSteps * kChainMaxUnits * pyc::kChainPad * sizeof(int);
+constexpr size_t kLine = (size_t)pyc::kChainPad * sizeof(int);  // one 128-byte counter line
+// done[] (one line per step), then the exit and error words
+constexpr size_t kChainCtlBytes = (size_t)(pyc::kChainMaxSteps + 2) * kLine;
+constexpr size_t kChainHeadBytes = kChainCtlBytes + (size_t)pyc::kChainMaxSteps * kChainMaxUnits * kLine;
 
+// Where everything of one chain launch lives, as byte offsets from the base of
+// its workspace: the done/exit/error lines, each step's arrival counters,
+// intermediate activations and split-K slots. [zero_lo, zero_hi) is what the
+// allocation-free launch clears before every launch (done, exit, counters).
 struct ChainLayout {
-    size_t act[pyc::kChainMaxSteps], part[pyc::kChainMaxSteps];
+    size_t done, exit, err;
+    size_t cnt[pyc::kChainMaxSteps], act[pyc::kChainMaxSteps], part[pyc::kChainMaxSteps];
+    size_t zero_lo, zero_hi;
     size_t total;
     W8Plan plan[pyc::kChainMaxSteps];
 };
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// -1: shape outside the chain kernel's preconditions.
-int chain_layout(int M, int nsteps, const int* N, const int* K, ChainLayout& L) {
+// -1: shape outside the chain kernel's preconditions. `compact` lays the
+// counters out for this shape only (the static scratch of the allocation-free
+// launch, cleared per launch); otherwise they sit in the workspace's fixed
+// head (which is zeroed once and re-armed by every complete launch).
+int chain_layout(int M, int nsteps, const int* N, const int* K, ChainLayout& L, bool compact = false) {
     if (M <= 0 || M > 32 || nsteps <= 0 || nsteps > pyc::kChainMaxSteps) return -1;
-    size_t off = kChainHeadBytes;
     for (int s = 0; s < nsteps; ++s) {
         if (N[s] <= 0 || K[s] <= 0 || N[s] % pyc::kW8Rows != 0 || K[s] % pyc::kQK != 0) return -1;
         if (N[s] / pyc::kW8Rows > kChainMaxUnits) return -1;
@@ -1053,6 +1062,30 @@ int chain_layout(int M, int nsteps, const int* N, const int* K, ChainLayout& L) 
         if ((size_t)N[s] * K[s] >= 0xFFFFFFFFull || (size_t)M * K[s] * 2 >= 0xFFFFFFFFull) return -1;
         L.plan[s] = w8_plan(N[s], K[s], cu_count());
         if (L.plan[s].max_slots > 8) return -1;
+    }
+    size_t off;
+    if (compact) {
+        // error line first, outside the cleared range: it stays set until read
+        L.err = 0;
+        L.done = kLine;
+        L.exit = kLine + (size_t)pyc::kChainMaxSteps * kLine;
+        L.zero_lo = L.done;
+        off = L.exit + kLine;
+        for (int s = 0; s < nsteps; ++s) {
+            L.cnt[s] = off;
+            off += (size_t)L.plan[s].units * kLine;
+        }
+        L.zero_hi = off;
+        off = align256(off);
+    } else {
+        L.done = 0;
+        L.exit = (size_t)pyc::kChainMaxSteps * kLine;
+        L.err = L.exit + kLine;
+        for (int s = 0; s < nsteps; ++s) L.cnt[s] = kChainCtlBytes + (size_t)s * kChainMaxUnits * kLine;
+        L.zero_lo = L.zero_hi = 0;
+        off = kChainHeadBytes;
+    }
+    for (int s = 0; s < nsteps; ++s) {
         L.act[s] = off;
         if (s + 1 < nsteps) off += align256((size_t)M * N[s] * 2);
     }
@@ -1077,6 +1110,55 @@ bool chain_reserve(size_t bytes) {
     ws.buf = nb;  // the old buffer is left allocated: in-flight launches may still use it
     ws.bytes = bytes;
     return true;
+}
+
+// Kernel arguments of a chain laid out by L at `ws`. -1 on a null operand.
+int chain_args(pyc::W8ChainArgs& a, const ChainLayout& L, uint8_t* ws, int M, int nsteps, const void* X,
+               const void* const* Wq, const float* const* scale, const int* N, const int* K, const int* relu,
+               void* Y) {
+    using namespace pyc;
+    a.nsteps = nsteps;
+    a.M = M;
+    a.done = (int*)(ws + L.done);
+    a.exit_cnt = (int*)(ws + L.exit);
+    a.err = (int*)(ws + L.err);
+    for (int s = 0; s < nsteps; ++s) {
+        W8ChainStep& P = a.st[s];
+        if (!Wq[s] || !scale[s]) return -1;
+        P.X = s == 0 ? (const uint16_t*)X : a.st[s - 1].Y;
+        P.W = (const uint8_t*)Wq[s];
+        P.scale = scale[s];
+        P.Y = s + 1 == nsteps ? (uint16_t*)Y : (uint16_t*)(ws + L.act[s]);
+        P.part = (float*)(ws + L.part[s]);
+        P.cnt = (int*)(ws + L.cnt[s]);
+        P.N = N[s];
+        P.K = K[s];
+        P.relu = relu[s] ? 1 : 0;
+        P.base = L.plan[s].base;
+        P.rem = L.plan[s].rem;
+        P.max_slots = L.plan[s].max_slots;
+        P.gs = L.plan[s].G;
+    }
+    return 0;
+}
+
+// One workgroup per CU (the LDS ring allows no second one), all resident
+// together. Ring depth: fewer loads in flight shorten the queueing that the
+// step boundary's round trips wait behind (PYC_CHAIN_STAGES overrides).
+int chain_kernel_launch(const pyc::W8ChainArgs& a, hipStream_t st) {
+    using namespace pyc;
+    static int stages = 0;
+    if (stages == 0) {
+        const char* e = getenv("PYC_CHAIN_STAGES");
+        const int v = e ? atoi(e) : 0;
+        stages = (v == 4 || v == 5 || v == 6 || v == 8) ? v : 6;
+    }
+    const dim3 grid(cu_count()), block(kCWaves * kWave);
+    if (stages == 4) hipLaunchKernelGGL(w8a16_chain_kernel<4>, grid, block, 0, st, a);
+    else if (stages == 5) hipLaunchKernelGGL(w8a16_chain_kernel<5>, grid, block, 0, st, a);
+    else if (stages == 6) hipLaunchKernelGGL(w8a16_chain_kernel<6>, grid, block, 0, st, a);
+    else hipLaunchKernelGGL(w8a16_chain_kernel<8>, grid, block, 0, st, a);
+    return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
 }  // namespace
@@ -1104,46 +1186,43 @@ extern "C" int pyc_hip_w8a16_chain_launch(int M, int nsteps, const void* X, cons
         if (cs != hipStreamCaptureStatusNone) return -3;  // reserve before capturing
         if (!chain_reserve(L.total)) return -2;
     }
-    uint8_t* ws = g_chainws[dev].buf;
     W8ChainArgs a;
-    a.nsteps = nsteps;
-    a.M = M;
-    int* ctl = (int*)ws;
-    a.done = ctl;
-    a.exit_cnt = ctl + kChainMaxSteps * kChainPad;
-    a.err = ctl + (kChainMaxSteps + 1) * kChainPad;
-    for (int s = 0; s < nsteps; ++s) {
-        W8ChainStep& P = a.st[s];
-        if (!Wq[s] || !scale[s]) return -1;
-        P.X = s == 0 ? (const uint16_t*)X : a.st[s - 1].Y;
-        P.W = (const uint8_t*)Wq[s];
-        P.scale = scale[s];
-        P.Y = s + 1 == nsteps ? (uint16_t*)Y : (uint16_t*)(ws + L.act[s]);
-        P.part = (float*)(ws + L.part[s]);
-        P.cnt = (int*)(ws + kChainCtlBytes) + (size_t)s * kChainMaxUnits * kChainPad;
-        P.N = N[s];
-        P.K = K[s];
-        P.relu = relu[s] ? 1 : 0;
-        P.base = L.plan[s].base;
-        P.rem = L.plan[s].rem;
-        P.max_slots = L.plan[s].max_slots;
-        P.gs = L.plan[s].G;
-    }
-    // one workgroup per CU (the LDS ring allows no second one), all resident together
-    // ring depth: fewer loads in flight shorten the queueing that the step
-    // boundary's round trips wait behind (PYC_CHAIN_STAGES overrides)
-    static int stages = 0;
-    if (stages == 0) {
-        const char* e = getenv("PYC_CHAIN_STAGES");
-        const int v = e ? atoi(e) : 0;
-        stages = (v == 4 || v == 5 || v == 6 || v == 8) ? v : 6;
-    }
-    const dim3 grid(cu_count()), block(kCWaves * kWave);
-    if (stages == 4) hipLaunchKernelGGL(w8a16_chain_kernel<4>, grid, block, 0, st, a);
-    else if (stages == 5) hipLaunchKernelGGL(w8a16_chain_kernel<5>, grid, block, 0, st, a);
-    else if (stages == 6) hipLaunchKernelGGL(w8a16_chain_kernel<6>, grid, block, 0, st, a);
-    else hipLaunchKernelGGL(w8a16_chain_kernel<8>, grid, block, 0, st, a);
-    return hipGetLastError() == hipSuccess ? 0 : -2;
+    if (chain_args(a, L, g_chainws[dev].buf, M, nsteps, X, Wq, scale, N, K, relu, Y) != 0) return -1;
+    return chain_kernel_launch(a, st);
+}
+
+// 1 when a chain of this shape meets the chain kernel's preconditions (the
+// ones pyc_hip_w8a16_chain_dispatch checks), 0 otherwise. Host only.
+extern "C" int pyc_hip_w8a16_chain_supported(int M, int nsteps, const int* N, const int* K) {
+    ChainLayout L;
+    return (N && K && chain_layout(M, nsteps, N, K, L) == 0) ? 1 : 0;
+}
+
+// Enqueues on `stream` a copy of the current device's chain timeout word into
+// *host_dst (pinned host memory, so the copy can be captured into a graph).
+// 0, or -1 when no chain workspace exists yet, -2 on a HIP error.
+extern "C" int pyc_hip_w8a16_chain_error_enqueue(int* host_dst, void* stream) {
+    using namespace pyc;
+    int dev = 0;
+    if (!host_dst || hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return -2;
+    W8ChainWorkspace& ws = g_chainws[dev];
+    if (!ws.buf) return -1;
+    const int* err = (const int*)ws.buf + (kChainMaxSteps + 1) * kChainPad;
+    return hipMemcpyAsync(host_dst, err, sizeof(int), hipMemcpyDeviceToHost, (hipStream_t)stream) == hipSuccess ? 0 : -2;
+}
+
+// Sets the current device's chain timeout word as a wait that ran out would,
+// so callers can test their failure handling without a kernel timing out.
+// Creates the workspace head if needed. 0, or -2 on a HIP error.
+extern "C" int pyc_hip_w8a16_chain_error_raise(void) {
+    using namespace pyc;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return -2;
+    if (!chain_reserve(kChainHeadBytes)) return -2;
+    int* err = (int*)g_chainws[dev].buf + (kChainMaxSteps + 1) * kChainPad;
+    const int one = 1;
+    if (hipMemcpy(err, &one, sizeof(int), hipMemcpyHostToDevice) != hipSuccess) return -2;
+    return 0;
 }
 
 // Reads (and with clear != 0 resets) the chain's timeout flag of the current

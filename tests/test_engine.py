@@ -512,14 +512,31 @@ def test_strict_mode_turns_fallback_into_error(monkeypatch):
 
 def test_unsupported_kind_reason(monkeypatch):
     monkeypatch.setenv("PYC_CUDA_SIMULATE_AVAILABLE", "1")
-    ops = [eu.op(abi.OP_INPUT, "x", (4,)), eu.op(abi.OP_GELU, "g", (), (0,)), eu.op(abi.OP_OUTPUT, "o", (4,), (1,))]
+    ops = [eu.op(abi.OP_INPUT, "x", (4,)), eu.op(abi.OP_REDUCE_SUM, "r", (), (0,)), eu.op(abi.OP_OUTPUT, "o", (1,), (1,))]
     mdl = eu.Model(eu.mine(), ops, backend=abi.BACKEND_CUDA)
-    st, _, s = mdl.run([np.ones(4, np.float32)], [(4,)])
+    st, _, s = mdl.run([np.ones(4, np.float32)], [(1,)])
     lf = eu.log_fields(mdl.log())
     mdl.close()
-    # GELU has no lowering anywhere: the CPU executor refuses it too
+    # REDUCE_SUM has no lowering anywhere: the CPU executor refuses it too
     assert st == abi.STATUS_RUNTIME_FAILED and lf["cuda_reason"] == "cpu_fallback_failed"
+    assert s.graph_break_reduce_sum_count == 1
+
+
+def test_graph_break_op_falls_back_to_cpu_executor(monkeypatch):
+    """GELU is a graph break for the reference (pass_manager.c:313-373) and its
+    executor refuses it; this engine's CPU executor runs it, so without a GPU
+    the module completes as a CPU fallback."""
+    import oracle
+    monkeypatch.setenv("PYC_CUDA_DISABLE", "1")
+    ops = [eu.op(abi.OP_INPUT, "x", (4,)), eu.op(abi.OP_GELU, "g", (), (0,)), eu.op(abi.OP_OUTPUT, "o", (4,), (1,))]
+    mdl = eu.Model(eu.mine(), ops, backend=abi.BACKEND_CUDA)
+    x = np.array([-2.0, -0.5, 0.0, 3.0], np.float32)
+    st, (out,), s = mdl.run([x], [(4,)])
+    lf = eu.log_fields(mdl.log())
+    mdl.close()
+    assert st == 0 and lf["cuda_fallback"] == "1" and lf["cuda_reason"] == "disabled_by_env"
     assert s.graph_break_gelu_count == 1
+    assert np.allclose(out, oracle.gelu_f64(x.astype(np.float64)), rtol=1e-6, atol=1e-7)
 
 
 def test_engine_wrapper_cpu_backend():

@@ -32,7 +32,7 @@ def _autotune(L, dtype, M, N, K):
 
 @pytest.mark.parametrize("dtype,expect", [(abi.DTYPE_BF16, {"hip_gemm_bf16_nn_256x256", "hip_gemm_bf16_nn_128x128",
                                                             "hip_gemm_bf16_nn", "cutlass_gemm_tensorcore_bf16"}),
-                                          (abi.DTYPE_F32, {"hip_gemm_f32_nn_64x64", "ada_gemm_k64_warp32_async_f32"}),
+                                          (abi.DTYPE_F32, {"hip_gemm_f32_nn_64x64"}),
                                           (abi.DTYPE_F16, {"hip_gemm_f16_nn"})])
 def test_autotune_direct(gpu, dtype, expect):
     n, syms, ms = _autotune(pyc_amd.lib(), dtype, 1024, 768, 512)
@@ -80,7 +80,9 @@ def test_run_model_autotune(gpu, dt, tmp_path, monkeypatch):
         if tune:
             assert st.autotune_saved == 1
             lines = [ln.split("|") for ln in db.read_text().splitlines() if ln.strip()]
-            assert len(lines) >= 2 and all(ln[0] == "matmul_fused" and float(ln[3]) > 0 for ln in lines)
+            # bf16 has four [K,N] variants, fp32 one distinct kernel
+            assert len(lines) >= (2 if dt == abi.DTYPE_BF16 else 1)
+            assert all(ln[0] == "matmul_fused" and float(ln[3]) > 0 for ln in lines)
             best = min(lines, key=lambda ln: float(ln[3]))[2]
             assert path.endswith(":" + best), (path, lines)
     for tune, y in outs.items():

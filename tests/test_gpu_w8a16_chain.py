@@ -93,6 +93,45 @@ def test_chain_decode_config(gpu):
         assert torch.equal(Y, Y2), f"input {seed}: a second launch differs"
 
 
+def test_chain_decode_config_vs_oracle(gpu):
+    """BASELINE config 5 end to end against the CPU oracle: 8 x [x(32x4096)
+    -> W_up(4096x11008, fp8) -> ReLU -> W_down(11008x4096, fp8)], x ~ N(0,1)
+    seed 9, layer l's weights ~ N(0, sqrt(2/K)) from seed 10+l quantized per
+    output channel (the bench's inputs), the whole chain in one launch. The
+    oracle runs the 16 layers in fp32 with bf16 activations between them
+    (threaded over output channels; the result does not depend on it).
+    Tolerance: max|got-ref| <= 2e-2 * max|ref|."""
+    import os
+    torch = gpu
+    L, M, D, F = 8, 32, 4096, 11008
+    g = torch.Generator(device="cuda").manual_seed(9)
+    x = torch.randn((M, D), generator=g, device="cuda").to(torch.bfloat16)
+    layers, host = [], []
+    for l in range(L):
+        gl = torch.Generator(device="cuda").manual_seed(10 + l)
+        w_up = torch.randn((D, F), generator=gl, device="cuda") * np.sqrt(2.0 / D)
+        w_dn = torch.randn((F, D), generator=gl, device="cuda") * np.sqrt(2.0 / F)
+        for w, relu in ((w_up, True), (w_dn, False)):
+            s = (w.abs().amax(0) / 448.0).clamp_min(1e-30)
+            q = (w / s).t().contiguous().to(torch.float8_e4m3fn).view(torch.uint8)
+            s = s.float().contiguous()
+            layers.append((q, s, relu))
+            host.append((q.cpu().numpy(), s.cpu().numpy(), relu))
+        del w_up, w_dn
+    y = torch.empty((M, D), dtype=torch.bfloat16, device="cuda")
+    pyc_amd.w8a16_chain(x, layers, y)
+    torch.cuda.synchronize()
+    assert pyc_amd.w8a16_chain_error() == 0
+    threads = min(16, len(os.sched_getaffinity(0)))
+    cur = host_bits16(x)
+    for wq, s, relu in host:
+        cur = oracle.w8a16_layer(cur, wq, s, relu, threads)
+    ref = oracle.bf16_to_f32(cur)
+    got = oracle.bf16_to_f32(host_bits16(y))
+    assert np.isfinite(got).all()
+    assert rel_max_err(got, ref) <= 2e-2
+
+
 def test_chain_graph_replay(gpu):
     """The chain launch captured in a graph and replayed with new inputs, with
     eager launches (of this and of another chain shape) in between: every
