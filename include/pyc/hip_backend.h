@@ -102,6 +102,27 @@ int pyc_hip_w8a16_chain_dispatch(
     const int* N, const int* K, const int* relu,
     void* Y, void* stream);
 
+/* pyc_hip_w8a16_chain_dispatch without any allocation. No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * arguments, kernels and results; the workspace (counters, intermediate
+ * activations, split-K slots) lives in a static device array of
+ * PYC_HIP_CHAIN_NOALLOC_SCRATCH_BYTES that each GPU the library runs on holds
+ * until the process ends, so no reserve call is needed before capturing it.
+ * Every call clears its counters with a small kernel on `stream` before the
+ * chain kernel (no memset node). Calls on one GPU share the array: calls
+ * whose executions overlap race. The timeout flag is read by
+ * pyc_hip_w8a16_chain_error. Returns 0, -1 on bad arguments, -2 on a HIP
+ * error, -3 when the chain's workspace exceeds the scratch size (config 5,
+ * 8 x [32x4096 -> 11008 -> 4096], needs 63.6 MiB). */
+#define PYC_HIP_CHAIN_NOALLOC_SCRATCH_BYTES (64u << 20)
+int pyc_hip_w8a16_chain_dispatch_noalloc(
+    const char* symbol,
+    int M, int nsteps,
+    const void* X, const void* const* Wq, const float* const* scale,
+    const int* N, const int* K, const int* relu,
+    void* Y, void* stream);
+
 /* Allocates the chain workspace for this shape on the current device; call it
  * outside stream capture before capturing a chain launch. 0, -1 (bad shape),
  * -2 (HIP error). */

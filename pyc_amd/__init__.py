@@ -43,6 +43,8 @@ def _declare(L: C.CDLL) -> None:
     L.pyc_hip_w8a16_gemm_dispatch.restype = I
     L.pyc_hip_w8a16_chain_dispatch.argtypes = [S, I, I, P, P, P, P, P, P, P, P]
     L.pyc_hip_w8a16_chain_dispatch.restype = I
+    L.pyc_hip_w8a16_chain_dispatch_noalloc.argtypes = [S, I, I, P, P, P, P, P, P, P, P]
+    L.pyc_hip_w8a16_chain_dispatch_noalloc.restype = I
     L.pyc_hip_w8a16_chain_reserve.argtypes = [I, I, P, P]
     L.pyc_hip_w8a16_chain_reserve.restype = I
     L.pyc_hip_w8a16_chain_error.argtypes = [I]

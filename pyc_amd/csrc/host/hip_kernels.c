@@ -39,6 +39,9 @@ int pyc_hip_w8a16_launch(int M, int N, int K, const void* X, const void* Wq, con
 int pyc_hip_w8a16_chain_launch(int M, int nsteps, const void* X, const void* const* Wq,
                                const float* const* scale, const int* N, const int* K, const int* relu,
                                void* Y, void* stream);
+int pyc_hip_w8a16_chain_launch_noalloc(int M, int nsteps, const void* X, const void* const* Wq,
+                                       const float* const* scale, const int* N, const int* K, const int* relu,
+                                       void* Y, void* stream);
 int pyc_hip_gelu_launch(int dtype, size_t n, const void* x, void* y, void* stream);
 int pyc_hip_layernorm_launch(int dtype, int rows, int D, float eps, const void* x, const void* gamma,
                              const void* beta, void* y, void* stream);
@@ -254,6 +257,14 @@ int pyc_hip_w8a16_chain_dispatch(const char* symbol, int M, int nsteps, const vo
     if (M <= 0 || M > 32 || nsteps <= 0 || !X || !Wq || !scale || !N || !K || !relu || !Y) return -1;
     const int rc = pyc_hip_w8a16_chain_launch(M, nsteps, X, Wq, scale, N, K, relu, Y, stream);
     return rc == -3 ? -1 : rc;
+}
+
+int pyc_hip_w8a16_chain_dispatch_noalloc(const char* symbol, int M, int nsteps, const void* X, const void* const* Wq,
+                                         const float* const* scale, const int* N, const int* K, const int* relu,
+                                         void* Y, void* stream) {
+    if (!symbol || strcmp(symbol, "hip_w8a16_chain_e4m3") != 0) return -1;
+    if (M <= 0 || M > 32 || nsteps <= 0 || !X || !Wq || !scale || !N || !K || !relu || !Y) return -1;
+    return pyc_hip_w8a16_chain_launch_noalloc(M, nsteps, X, Wq, scale, N, K, relu, Y, stream);
 }
 
 /* ---------------------------------------------------------------- GELU / LayerNorm */

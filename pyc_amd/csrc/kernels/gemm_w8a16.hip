@@ -33,6 +33,8 @@
 // Without a workspace every workgroup owns whole units instead.
 #include <stdlib.h>
 
+#include <mutex>
+
 #include "common.hpp"
 #include "lds_dma.hpp"
 
@@ -1191,6 +1193,70 @@ extern "C" int pyc_hip_w8a16_chain_launch(int M, int nsteps, const void* X, cons
     return chain_kernel_launch(a, st);
 }
 
+// ---------------------------------------------------------------------------
+// Allocation-free chain launch. The workspace is `scratch`, a file-scope
+// device array of kNoAllocScratchBytes that every GPU the library runs on
+// holds until the process ends. Its device address is looked up once per
+// device (hipGetSymbolAddress, with that device current) and kept per device:
+// on the host the array's name stands for no device address. Each launch
+// first clears the step, exit and arrival counters of its layout with a fill
+// kernel (no memset node, so it can be captured), then runs the same chain
+// kernel as pyc_hip_w8a16_chain_launch. The timeout word sits outside the
+// cleared range and is read by pyc_hip_w8a16_chain_error. Calls that overlap
+// on one GPU share the array and race.
+constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+
+uint8_t* g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_lock;
+
+// Device address of the current device's scratch array; nullptr on a HIP error.
+uint8_t* scratch_base(int dev) {
+    std::lock_guard<std::mutex> g(g_scratch_lock);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
+        g_scratch_ptr[dev] = (uint8_t*)p;
+    }
+    return g_scratch_ptr[dev];
+}
+
+__global__ void zero_words_kernel(uint32_t* __restrict__ p, int n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+}  // namespace
+
+extern "C" int pyc_hip_w8a16_chain_launch_noalloc(int M, int nsteps, const void* X, const void* const* Wq,
+                                                  const float* const* scale, const int* N, const int* K,
+                                                  const int* relu, void* Y, void* stream) {
+    using namespace pyc;
+    ChainLayout L;
+    if (!N || !K || !Wq || !scale || !relu || !X || !Y || chain_layout(M, nsteps, N, K, L, true) != 0) return -1;
+    if (L.total > kNoAllocScratchBytes) return -3;  // larger than the static scratch
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return -2;
+    uint8_t* base = scratch_base(dev);
+    if (!base) return -2;
+    W8ChainArgs a;
+    if (chain_args(a, L, base, M, nsteps, X, Wq, scale, N, K, relu, Y) != 0) return -1;
+    hipStream_t st = (hipStream_t)stream;
+    const int words = (int)((L.zero_hi - L.zero_lo) / sizeof(uint32_t));
+    hipLaunchKernelGGL(zero_words_kernel, dim3((words + 255) / 256 < 256 ? (words + 255) / 256 : 256), dim3(256), 0,
+                       st, (uint32_t*)(base + L.zero_lo), words);
+    if (hipGetLastError() != hipSuccess) return -2;
+    return chain_kernel_launch(a, st);
+}
+
+// Error word of the allocation-free launch on device dev, or nullptr when that
+// launch never ran there.
+static int* noalloc_err_word(int dev) {
+    std::lock_guard<std::mutex> g(g_scratch_lock);
+    return g_scratch_ptr[dev] ? (int*)g_scratch_ptr[dev] : nullptr;  // compact layout: err at offset 0
+}
+
 // 1 when a chain of this shape meets the chain kernel's preconditions (the
 // ones pyc_hip_w8a16_chain_dispatch checks), 0 otherwise. Host only.
 extern "C" int pyc_hip_w8a16_chain_supported(int M, int nsteps, const int* N, const int* K) {
@@ -1233,14 +1299,19 @@ extern "C" int pyc_hip_w8a16_chain_error(int clear) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return -2;
     W8ChainWorkspace& ws = g_chainws[dev];
-    if (!ws.buf) return 0;
+    int* words[2] = {ws.buf ? (int*)ws.buf + (kChainMaxSteps + 1) * kChainPad : nullptr, noalloc_err_word(dev)};
+    if (!words[0] && !words[1]) return 0;
     if (hipDeviceSynchronize() != hipSuccess) return -2;
-    int* err = (int*)ws.buf + (kChainMaxSteps + 1) * kChainPad;
-    int v = 0;
-    if (hipMemcpy(&v, err, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess) return -2;
-    if (clear && v != 0) {
-        const int z = 0;
-        if (hipMemcpy(err, &z, sizeof(int), hipMemcpyHostToDevice) != hipSuccess) return -2;
+    int any = 0;
+    for (int* err : words) {
+        int v = 0;
+        if (!err) continue;
+        if (hipMemcpy(&v, err, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess) return -2;
+        if (clear && v != 0) {
+            const int z = 0;
+            if (hipMemcpy(err, &z, sizeof(int), hipMemcpyHostToDevice) != hipSuccess) return -2;
+        }
+        any |= v != 0;
     }
-    return v != 0 ? 1 : 0;
+    return any ? 1 : 0;
 }
