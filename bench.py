@@ -9,12 +9,20 @@ resident operands. Prints ONE JSON line.
 
     python bench.py [--steps K] [--warmup W] [--workload NAME]
 
+The metric names bf16 GEMM and attention, so the default line also carries
+two nested blocks: "attention" (config 3, causal [8,32,2048,128] bf16, with
+its own roofline and CPU baseline) and "engine_cfg1" (config 1 through
+pyc_compile_model/pyc_run_model with device-resident tensors, with the
+reference bench driver's fields under "engine": execution path, profile,
+latency). --no-extras leaves them out.
+
 Other workloads (--workload) measure the remaining BASELINE configs for the
-record; they are not the bench line the driver reads by default.
-`engine_cfg1` runs config 1 through pyc_compile_model/pyc_run_model itself
-(device-resident tensors) and adds the reference bench driver's fields under
-"engine". Every line carries "latency_ms" (mean/p50/p95/min/max of the
-per-launch device times, or of the pyc_run_model wall times for the engine).
+record; they are not the bench line the driver reads by default. Every line
+carries "latency_ms" (mean/p50/p95/min/max of the per-launch device times, or
+of the pyc_run_model wall times for the engine) and "settle": before the
+warmup steps each workload runs back to back for --settle-ms (default 400 ms)
+so the timed steps see the clock the card holds under sustained load, not an
+idle card's ramp.
 
 The cpu_baseline leg times the reference's own CPU executor (the C11 engine
 built from the reference sources into oracle/_ref/libpyc_ref.so, through
@@ -48,10 +56,33 @@ def log(*a):
 # ---------------------------------------------------------------- timing helpers
 
 
-def time_launches(torch, launch, steps: int, warmup: int):
-    """Warm up, then time `steps` launches: total bracketed by synchronize, and
-    each launch between HIP events recorded on the stream it runs on."""
+def settle(torch, launch, ms: float) -> dict:
+    """Run the launch back to back for `ms` of wall time before the warmup
+    steps. An idle card's engine clock ramps up over the first tens to
+    hundreds of milliseconds of load; without this the few warmup steps a
+    short run asks for would be timed at a clock the card does not hold under
+    sustained load. Untimed; reported as "settle"."""
+    t0 = time.perf_counter()
+    n = 0
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(8):
+            launch()
+        torch.cuda.synchronize()
+        n += 8
+    return {"ms": (time.perf_counter() - t0) * 1e3, "launches": n}
+
+
+_LAST_SETTLE: dict = {}
+
+
+def time_launches(torch, launch, steps: int, warmup: int, settle_ms: float = 0.0):
+    """Settle the clock, warm up, then time `steps` launches: total bracketed
+    by synchronize, and each launch between HIP events recorded on the stream
+    it runs on."""
     stream = torch.cuda.current_stream()
+    _LAST_SETTLE.clear()
+    if settle_ms > 0:
+        _LAST_SETTLE.update(settle(torch, launch, settle_ms))
     for _ in range(warmup):
         launch()
     torch.cuda.synchronize()
@@ -102,14 +133,17 @@ def _host_cores() -> int:
         return os.cpu_count() or 1
 
 
-def cpu_baseline_gemm(a_rows_f32: np.ndarray, b_kn_f32: np.ndarray, full_flops: float, sample_desc: str):
+def cpu_baseline_gemm(a_rows_f32: np.ndarray, b_kn_f32: np.ndarray, full_flops: float, sample_desc: str,
+                      threads: int | None = None):
     """Time the reference CPU executor on a[rows] @ b (fp32) and scale to the
     metric's unit (TFLOP/s on the full workload's FLOP count; the per-row cost
-    is constant so throughput extrapolates linearly)."""
+    is constant so throughput extrapolates linearly). threads: the executor's
+    PYC_NUM_THREADS (default min(cores, 32), the reference's cap; 1 is the
+    reference default)."""
     rows, k = a_rows_f32.shape
     n = b_kn_f32.shape[1]
     flops = 2.0 * rows * k * n
-    threads = min(_host_cores(), 32)
+    threads = threads or min(_host_cores(), 32)
     try:
         from tests import refengine
         use_ref = refengine.available()
@@ -159,7 +193,7 @@ def wl_gemm_bf16(torch, args):
     Cd = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
     sym = args.symbol or "hip_gemm_bf16_nt"
     launch = lambda: pyc_amd.gemm(sym, A, B, Cd, M, N, K)  # noqa: E731
-    ms_step, ms_kernel, _ = time_launches(torch, launch, args.steps, args.warmup)
+    ms_step, ms_kernel, _ = time_launches(torch, launch, args.steps, args.warmup, args.settle_ms)
     flops = 2.0 * M * N * K
     value = flops / (ms_step * 1e-3) / 1e12
     achieved = flops / (ms_kernel * 1e-3) / 1e12
@@ -187,6 +221,11 @@ def wl_gemm_bf16(torch, args):
         got = Cd[ridx].float().cpu().numpy()
         res["parity_sample_max_rel_err"] = float(np.abs(got - out).max() / np.abs(out).max())
         res["speedup_vs_cpu"] = value / cpu["value"]
+        # the reference executor's default (PYC_NUM_THREADS unset): one thread
+        n1 = max(1, args.cpu_rows // 16)
+        cpu1, _ = cpu_baseline_gemm(a_rows[:n1], b_kn, flops,
+                                    f"{n1} of {M} rows of the 8192^3 GEMM, fp32 executor, 1 thread", threads=1)
+        res["cpu_baseline_1thread"] = cpu1
         del oracle
     return res
 
@@ -202,7 +241,7 @@ def wl_gemm_f32_cfg1(torch, args):
     Y = torch.empty((M, N), dtype=torch.float32, device="cuda")
     epi = pyc_amd.abi.EPI_BIAS | pyc_amd.abi.EPI_RELU
     launch = lambda: pyc_amd.gemm("hip_gemm_f32_nn_64x64", X, W, Y, M, N, K, bias=Bv, epilogue=epi)  # noqa: E731
-    ms_step, ms_kernel, _ = time_launches(torch, launch, args.steps, args.warmup)
+    ms_step, ms_kernel, _ = time_launches(torch, launch, args.steps, args.warmup, args.settle_ms)
     flops = 2.0 * M * N * K + 2.0 * M * N
     value = flops / (ms_step * 1e-3) / 1e12
     res = {
@@ -253,13 +292,40 @@ def wl_decode_chain(torch, args):
         pyc_amd.w8a16_chain(x, chain_layers, y, stream=s.cuda_stream)
         graph.capture_end()
     torch.cuda.synchronize()
-    ms_step, ms_kernel, _ = time_launches(torch, graph.replay, args.steps, args.warmup)
+    ms_step, ms_kernel, _ = time_launches(torch, graph.replay, args.steps, args.warmup, args.settle_ms)
     if pyc_amd.w8a16_chain_error() != 0:
         raise RuntimeError("decode chain: a workgroup timed out waiting (output invalid)")
     weight_bytes = L * (2 * D * F + 4 * (F + D))
     bytes_replay = L * (2 * D * F + 4 * F + 4 * D + M * D * 2 + 2 * M * F * 2 + M * D * 2)
     gbs = bytes_replay / (ms_step * 1e-3) / 1e9
-    return {
+    extra = {}
+    if not args.no_cpu:
+        # CPU leg: the oracle's fp8-weight layer (the reference has no fp8
+        # executor), the whole 16-layer chain on the host cores, and one
+        # layer on one thread (extrapolated to the chain)
+        import oracle
+        host = [(q.cpu().numpy(), s_.cpu().numpy(), relu) for q, s_, relu in chain_layers]
+        xh = x.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+        threads = min(_host_cores(), 32)
+        t0 = time.perf_counter()
+        cur = xh
+        for q, s_, relu in host:
+            cur = oracle.w8a16_layer(cur, q, s_, relu, threads)
+        dt = time.perf_counter() - t0
+        extra["cpu_baseline"] = {"value": bytes_replay / dt / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+                                 "sample": f"the whole 16-layer chain (one replay), oracle fp8-weight layer in fp32 "
+                                           f"threaded over output channels, {dt:.2f} s"}
+        t0 = time.perf_counter()
+        oracle.w8a16_layer(xh, host[0][0], host[0][1], True, 1)
+        dt1 = (time.perf_counter() - t0) * len(host)
+        extra["cpu_baseline_1thread"] = {"value": bytes_replay / dt1 / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+                                         "sample": f"one 32x4096x11008 layer on 1 thread, {dt1 / len(host):.2f} s, "
+                                                   "extrapolated to the 16 layers"}
+        got = oracle.bf16_to_f32(y.contiguous().view(torch.int16).cpu().numpy().view(np.uint16))
+        ref = oracle.bf16_to_f32(cur)
+        extra["parity_sample_max_rel_err"] = float(np.abs(got - ref).max() / np.abs(ref).max())
+        extra["speedup_vs_cpu"] = gbs / extra["cpu_baseline"]["value"]
+    return {**extra,
         "value": gbs, "unit": "GB/s", "ms_per_step": ms_step, "dtype": "fp8-e4m3 weights, bf16 activations",
         "config": {"workload": "decode_w8a16_chain_8x(32x4096x11008)", "replay": "hipGraph", "launches": 1,
                    "kernel": "w8a16_chain_kernel (16 GEMM steps in one persistent launch)"},
@@ -280,7 +346,7 @@ def wl_attention(torch, args):
     O = torch.empty_like(Q)
     scale = 1.0 / np.sqrt(D)
     launch = lambda: pyc_amd.attention("hip_attention_bf16", Q, K, V, O, True, scale)  # noqa: E731
-    ms_step, ms_kernel, _ = time_launches(torch, launch, args.steps, args.warmup)
+    ms_step, ms_kernel, _ = time_launches(torch, launch, args.steps, args.warmup, args.settle_ms)
     flops = 2.0 * B * H * S * S * D  # causal FA convention (half of 4*B*H*S^2*D)
     res = {
         "value": flops / (ms_step * 1e-3) / 1e12, "unit": "TFLOP/s", "ms_per_step": ms_step, "dtype": "bf16",
@@ -291,15 +357,29 @@ def wl_attention(torch, args):
     }
     if not args.no_cpu:
         import oracle
-        q, k, v = (t[0:1, 0:1].float().cpu().numpy() for t in (Q, K, V))
+        from concurrent.futures import ThreadPoolExecutor
+        threads = min(_host_cores(), 32, H)
+        q, k, v = (t[0:1, 0:threads].float().cpu().numpy() for t in (Q, K, V))
+        # the oracle's attention per (b,h) head, one head per thread (its C
+        # loop runs without the GIL)
         t0 = time.perf_counter()
-        ref = oracle.attention_f32(q, k, v, True, scale)
+        with ThreadPoolExecutor(threads) as ex:
+            parts = list(ex.map(lambda h: oracle.attention_f32(q[:, h:h + 1], k[:, h:h + 1], v[:, h:h + 1], True,
+                                                               scale), range(threads)))
         dt = time.perf_counter() - t0
-        res["cpu_baseline"] = {"value": 2.0 * S * S * D / dt / 1e12, "unit": "TFLOP/s", "cores": 1,
-                               "kind": "port", "sample": f"1 of {B * H} (b,h) heads, oracle fp32 attention, "
-                                                          f"{dt:.2f} s, extrapolated linearly"}
-        got = O[0:1, 0:1].float().cpu().numpy()
+        ref = np.concatenate(parts, axis=1)
+        res["cpu_baseline"] = {"value": flops * threads / (B * H) / dt / 1e12, "unit": "TFLOP/s", "cores": threads,
+                               "kind": "port", "sample": f"{threads} of {B * H} (b,h) heads, oracle fp32 attention, "
+                                                         f"one head per thread, {dt:.2f} s, extrapolated linearly"}
+        t0 = time.perf_counter()
+        oracle.attention_f32(q[:, 0:1], k[:, 0:1], v[:, 0:1], True, scale)
+        dt1 = time.perf_counter() - t0
+        res["cpu_baseline_1thread"] = {"value": flops / (B * H) / dt1 / 1e12, "unit": "TFLOP/s", "cores": 1,
+                                       "kind": "port", "sample": f"1 of {B * H} heads on 1 thread, {dt1:.2f} s, "
+                                                                 "extrapolated linearly"}
+        got = O[0:1, 0:threads].float().cpu().numpy()
         res["parity_sample_max_rel_err"] = float(np.abs(got - ref).max() / np.abs(ref).max())
+        res["speedup_vs_cpu"] = res["value"] / res["cpu_baseline"]["value"]
     return res
 
 
@@ -313,7 +393,7 @@ def wl_conv(torch, args):
     Bv = 0.01 * torch.randn(K, generator=gb, device="cuda")
     Y = torch.empty((N, H, W, K), dtype=torch.bfloat16, device="cuda")
     launch = lambda: pyc_amd.conv2d("hip_conv2d_bf16", X, Wd, Y, pad=(1, 1), stride=(1, 1), bias=Bv, relu=True)  # noqa: E731
-    ms_step, ms_kernel, _ = time_launches(torch, launch, args.steps, args.warmup)
+    ms_step, ms_kernel, _ = time_launches(torch, launch, args.steps, args.warmup, args.settle_ms)
     flops = 2.0 * N * H * W * K * C * 9
     res = {
         "value": flops / (ms_step * 1e-3) / 1e12, "unit": "TFLOP/s", "ms_per_step": ms_step, "dtype": "bf16",
@@ -374,6 +454,9 @@ def wl_engine_cfg1(torch, args):
             raise RuntimeError(f"pyc_run_model failed ({rc}): {st.execution_path.decode()}")
         return st
 
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < args.settle_ms:
+        call()
     for _ in range(args.warmup):
         call()
     stats, wall = [], []
@@ -444,7 +527,8 @@ def wl_gelu(torch, args):
     n = 64 << 20
     x = torch.randn(n, generator=torch.Generator(device="cuda").manual_seed(13), device="cuda").to(torch.bfloat16)
     y = torch.empty_like(x)
-    ms_step, ms_kernel, _ = time_launches(torch, lambda: pyc_amd.gelu(x, y), args.steps, args.warmup)
+    ms_step, ms_kernel, _ = time_launches(torch, lambda: pyc_amd.gelu(x, y), args.steps, args.warmup,
+                                          args.settle_ms)
     return _eltwise_line("gelu", {"workload": "gelu_bf16_64Mi"}, 4.0 * n, ms_step, ms_kernel)
 
 
@@ -460,7 +544,7 @@ def wl_layernorm(torch, args):
     beta = torch.randn(D, generator=g, device="cuda").to(torch.bfloat16)
     y = torch.empty_like(x)
     ms_step, ms_kernel, _ = time_launches(torch, lambda: pyc_amd.layernorm(x, y, gamma, beta), args.steps,
-                                          args.warmup)
+                                          args.warmup, args.settle_ms)
     return _eltwise_line("layernorm", {"workload": "layernorm_bf16_16384x4096_affine"},
                          4.0 * rows * D + 4.0 * D, ms_step, ms_kernel)
 
@@ -474,15 +558,19 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
-    # The GPU clock of an idle card ramps up over the first tens of
-    # milliseconds of load: 10 warmup launches left the attention kernel's
-    # timed steps 20% slow. 100 launches cover the ramp for every workload.
-    ap.add_argument("--warmup", type=int, default=100)
+    # The GPU clock of an idle card ramps up over the first tens to hundreds
+    # of milliseconds of load: the settle phase (--settle-ms) runs first, then
+    # the warmup steps.
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="gemm_bf16", choices=sorted(WORKLOADS))
     ap.add_argument("--symbol", default=None, help="GEMM kernel symbol override")
     ap.add_argument("--cpu-rows", type=int, default=1024,
                     help="rows of the GEMM the CPU executor computes (about 10-30 CPU-seconds)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="default workload only: skip the nested attention and engine blocks")
+    ap.add_argument("--settle-ms", type=float, default=400.0,
+                    help="untimed back-to-back launches before the warmup steps (clock ramp)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -498,16 +586,33 @@ def main() -> int:
     info = pyc_amd.device_info()
     log(f"device {info.gcn_arch.decode()} CUs={info.compute_units} sclk={info.clock_khz / 1e3:.0f} MHz")
     res = WORKLOADS[args.workload](torch, args)
+    latency = res.get("latency_ms") or dict(_LAST_LATENCY)
+    settled = dict(_LAST_SETTLE)
+    nested = {}
+    if args.workload == "gemm_bf16" and not args.no_extras:
+        # The metric names bf16 GEMM and attention: config 3 rides along as a
+        # nested block with its own roofline and CPU baseline, and config 1
+        # through pyc_compile_model/pyc_run_model carries the reference bench
+        # driver's engine fields (execution path, profile).
+        att = wl_attention(torch, args)
+        att["latency_ms"] = dict(_LAST_LATENCY)
+        att["settle"] = dict(_LAST_SETTLE)
+        nested["attention"] = att
+        eng = wl_engine_cfg1(torch, args)
+        nested["engine_cfg1"] = eng
     line = {
         "metric": METRIC, "value": res["value"], "unit": res["unit"], "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": True,
         "scaling": "weak", "vs_baseline": res.get("vs_baseline"), "dtype": res["dtype"], "data": "synthetic",
         "config": res["config"], "roofline": res["roofline"],
     }
-    line["latency_ms"] = res.get("latency_ms") or dict(_LAST_LATENCY)
-    for k in ("cpu_baseline", "parity_sample_max_rel_err", "speedup_vs_cpu", "baseline_ref", "engine"):
+    line["latency_ms"] = latency
+    line["settle"] = settled
+    for k in ("cpu_baseline", "cpu_baseline_1thread", "parity_sample_max_rel_err", "speedup_vs_cpu", "baseline_ref",
+              "engine"):
         if k in res:
             line[k] = res[k]
+    line.update(nested)
     line["device"] = {"arch": info.gcn_arch.decode(), "cus": info.compute_units,
                       "sclk_mhz": info.clock_khz / 1e3}
     print(json.dumps(line), flush=True)
