@@ -230,6 +230,32 @@ def wl_gemm_bf16(torch, args):
     return res
 
 
+def wl_gemm_bf16_nn(torch, args):
+    """Config 2's GEMM with B stored row-major [K,N]: the layout of the IR's
+    MATMUL and of the reference's default bf16 symbol
+    cutlass_gemm_tensorcore_bf16 (reference gemm/kernel.cu:175-187), on the
+    persistent kernel's [K,N] form."""
+    import pyc_amd
+    M = N = K = 8192
+    g1 = torch.Generator(device="cuda").manual_seed(1)
+    g2 = torch.Generator(device="cuda").manual_seed(2)
+    A = (torch.randn((M, K), generator=g1, device="cuda") / np.sqrt(K)).to(torch.bfloat16)
+    B = (torch.randn((K, N), generator=g2, device="cuda") / np.sqrt(K)).to(torch.bfloat16)
+    Cd = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    sym = args.symbol or "cutlass_gemm_tensorcore_bf16"
+    launch = lambda: pyc_amd.gemm(sym, A, B, Cd, M, N, K)  # noqa: E731
+    ms_step, ms_kernel, _ = time_launches(torch, launch, args.steps, args.warmup, args.settle_ms)
+    flops = 2.0 * M * N * K
+    return {
+        "value": flops / (ms_step * 1e-3) / 1e12, "unit": "TFLOP/s", "ms_per_step": ms_step, "dtype": "bf16",
+        "config": {"workload": "gemm_bf16_nn_8192x8192x8192", "kernel": sym, "M": M, "N": N, "K": K,
+                   "layout": "A row-major [M,K], B row-major [K,N], C row-major bf16"},
+        "roofline": {"bound": "mfma", "achieved": flops / (ms_kernel * 1e-3) / 1e12, "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": flops / (ms_kernel * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+                     "traffic": load_traffic("gemm_bf16_nn_8192"), "kernel_ms": ms_kernel},
+    }
+
+
 def wl_gemm_f32_cfg1(torch, args):
     import pyc_amd
     M = N = K = 1024
@@ -549,7 +575,7 @@ def wl_layernorm(torch, args):
                          4.0 * rows * D + 4.0 * D, ms_step, ms_kernel)
 
 
-WORKLOADS = {"gemm_bf16": wl_gemm_bf16, "gemm_f32_cfg1": wl_gemm_f32_cfg1, "decode_chain": wl_decode_chain,
+WORKLOADS = {"gemm_bf16": wl_gemm_bf16, "gemm_bf16_nn": wl_gemm_bf16_nn, "gemm_f32_cfg1": wl_gemm_f32_cfg1, "decode_chain": wl_decode_chain,
              "attention": wl_attention, "conv": wl_conv, "engine_cfg1": wl_engine_cfg1,
              "gelu": wl_gelu, "layernorm": wl_layernorm}
 

@@ -1695,8 +1695,9 @@ int pyc_hip_autotune_gemm(pyc_dtype dtype, int M, int N, int K, int iters, char*
     /* one entry per distinct kernel: the reference's fp32 alias
      * ada_gemm_k64_warp32_async_f32 runs hip_gemm_f32_nn_64x64's kernel with a
      * narrower epilogue, so timing it would only pick between equal launches */
-    static const char* const cands[] = {"hip_gemm_bf16_nn_256x256", "hip_gemm_bf16_nn_128x128", "hip_gemm_bf16_nn",
-                                        "cutlass_gemm_tensorcore_bf16", "hip_gemm_f16_nn", "hip_gemm_f32_nn_64x64"};
+    static const char* const cands[] = {"hip_gemm_bf16_nn_256x256_lds", "hip_gemm_bf16_nn_256x256",
+                                        "hip_gemm_bf16_nn_128x128", "hip_gemm_bf16_nn", "cutlass_gemm_tensorcore_bf16",
+                                        "hip_gemm_f16_nn_256x256_lds", "hip_gemm_f16_nn", "hip_gemm_f32_nn_64x64"};
     const size_t eb = dtype_bytes(dtype);
     void *a = NULL, *b = NULL, *c = NULL;
     hipStream_t s = NULL;

@@ -26,6 +26,8 @@ int pyc_hip_gemm_half_launch(int is_bf16, int b_trans, int tile, int M, int N, i
                              const float* bias, int epi, void* stream);
 int pyc_hip_gemm_nt_lds_launch(int is_bf16, int M, int N, int K, const void* A, const void* B, void* C,
                                float alpha, float beta, const float* bias, int epi, void* stream);
+int pyc_hip_gemm_nn_lds_launch(int is_bf16, int M, int N, int K, const void* A, const void* B, void* C,
+                               float alpha, float beta, const float* bias, int epi, void* stream);
 int pyc_hip_gemm_f32_launch(int b_trans, int M, int N, int K, const void* A, const void* B,
                             void* C, float alpha, float beta, const float* bias, int epi,
                             void* stream);
@@ -57,7 +59,7 @@ typedef struct {
     int kind;
     int dtype;
     int b_trans;  /* GEMM: B stored [N,K] */
-    int tile;     /* GEMM half tile edge; 0 = choose by shape; -1 = direct-LDS 8-wave NT kernel */
+    int tile;     /* GEMM half tile edge; 0 = choose by shape; -1 = the persistent LDS-DMA kernel (4 waves, 256 x 256) */
     int unit_epilogue_only; /* alpha must be 1 and beta 0 */
     int priority;
     double occupancy;      /* waves per SIMD / 8 for the variant's launch bounds */
@@ -71,12 +73,14 @@ static const hip_variant k_variants[] = {
     {"matmul", "hip_gemm_bf16_nt_256x256_lds", VK_GEMM, VT_BF16, 1, -1, 0, 125, 0.25, 131072, 2, PYC_KERNEL_WORKLOAD_LARGE_SQUARE},
     {"matmul", "hip_gemm_bf16_nt_256x256", VK_GEMM, VT_BF16, 1, 256, 0, 120, 0.125, 131072, 3, PYC_KERNEL_WORKLOAD_LARGE_SQUARE},
     {"matmul", "hip_gemm_bf16_nt_128x128", VK_GEMM, VT_BF16, 1, 128, 0, 110, 0.25, 65536, 2, PYC_KERNEL_WORKLOAD_SQUARE},
+    {"matmul", "hip_gemm_bf16_nn_256x256_lds", VK_GEMM, VT_BF16, 0, -1, 0, 118, 0.25, 163840, 2, PYC_KERNEL_WORKLOAD_LARGE_SQUARE},
     {"matmul", "hip_gemm_bf16_nn_256x256", VK_GEMM, VT_BF16, 0, 256, 0, 115, 0.125, 131072, 3, PYC_KERNEL_WORKLOAD_LARGE_SQUARE},
     {"matmul", "hip_gemm_bf16_nn_128x128", VK_GEMM, VT_BF16, 0, 128, 0, 105, 0.25, 65536, 2, PYC_KERNEL_WORKLOAD_SQUARE},
     {"matmul", "hip_gemm_bf16_nt", VK_GEMM, VT_BF16, 1, 0, 0, 100, 0.125, 131072, 3, PYC_KERNEL_WORKLOAD_ANY},
     {"matmul", "hip_gemm_bf16_nn", VK_GEMM, VT_BF16, 0, 0, 0, 100, 0.125, 131072, 3, PYC_KERNEL_WORKLOAD_ANY},
     /* fp16 MFMA GEMM */
     {"matmul", "hip_gemm_f16_nt_256x256_lds", VK_GEMM, VT_F16, 1, -1, 0, 96, 0.25, 131072, 2, PYC_KERNEL_WORKLOAD_LARGE_SQUARE},
+    {"matmul", "hip_gemm_f16_nn_256x256_lds", VK_GEMM, VT_F16, 0, -1, 0, 96, 0.25, 163840, 2, PYC_KERNEL_WORKLOAD_LARGE_SQUARE},
     {"matmul", "hip_gemm_f16_nt", VK_GEMM, VT_F16, 1, 0, 0, 95, 0.125, 131072, 3, PYC_KERNEL_WORKLOAD_ANY},
     {"matmul", "hip_gemm_f16_nn", VK_GEMM, VT_F16, 0, 0, 0, 95, 0.125, 131072, 3, PYC_KERNEL_WORKLOAD_ANY},
     /* fp32 MFMA GEMM (true fp32) */
@@ -171,6 +175,19 @@ static int gemm_run(const hip_variant* v, int M, int N, int K, const void* A, co
                                                   epilogue, stream);
         if (rc != 1) {
             return rc;
+        }
+    }
+    /* The persistent LDS kernel with a [K,N] operand (transpose reads) takes
+     * large NN shapes; the _lds symbols name it alone (-1 outside its
+     * preconditions), the shape-chosen symbols fall back to the tiled kernels. */
+    if (!v->b_trans && (v->tile == -1 || (v->tile == 0 && pick_half_tile(M, N) == 256))) {
+        const int rc = pyc_hip_gemm_nn_lds_launch(v->dtype == VT_BF16, M, N, K, A, B, C, alpha, beta, bias,
+                                                  epilogue, stream);
+        if (rc != 1) {
+            return rc;
+        }
+        if (v->tile == -1) {
+            return -1;
         }
     }
     return pyc_hip_gemm_half_launch(v->dtype == VT_BF16, v->b_trans, v->tile > 0 ? v->tile : pick_half_tile(M, N),

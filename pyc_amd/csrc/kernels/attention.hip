@@ -109,12 +109,7 @@ __device__ inline float other_half(float x, int xaddr) {
 // row (key0 + L/4), columns (d0 + 4*(L%4)) .. +3 of a row-major [key][d] tile
 // therefore gets, in lane i, the four keys key0..key0+3 of column d0 + i: the
 // V^T operand of O^T = V^T P^T, read from untransposed V.
-typedef short v4i16_t __attribute__((ext_vector_type(4)));
-__device__ inline u32x2 lds_read_tr16(const uint16_t* p) {
-    const v4i16_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (__attribute__((address_space(3))) v4i16_t*)(__attribute__((address_space(3))) uint16_t*)p);
-    return __builtin_bit_cast(u32x2, v);
-}
+// (lds_read_tr16 in lds_dma.hpp)
 
 // Work. A unit is, with a causal mask, the pair of q-blocks nqb-1-u and u of
 // one head (equal work for every unit), else one q-block; each q-block is a

@@ -41,6 +41,16 @@ constexpr int kD_BM = 256, kD_BN = 256;
 // (rocprofv3 SQ_LDS_BANK_CONFLICT reads 0 for these kernels).
 __device__ inline int d_swz(int row, int chunk) { return chunk ^ (row & 7); }
 
+// [K,N] right operand (NN GEMM): its stage is 64 k-rows of 256 n (512-byte
+// rows, 32 chunks of 16 bytes), and the MFMA fragment (16 n x 32 k, 8
+// consecutive k per lane) comes from two transpose reads (lds_read_tr16) of 4
+// k-rows each. One such read by 32 lanes (one LDS pass) touches 32 bytes of
+// each of the k-rows r0..r0+3 and r0+8..r0+11; storing logical chunk c of
+// k-row r at chunk c ^ nn_swz(r) puts those 8 segments into the 8 distinct
+// 32-byte bank groups of a 256-byte bank window. nn_swz is even, so a 32-byte
+// segment (a chunk pair) stays contiguous.
+__device__ inline int nn_swz(int row) { return 2 * (row & 3) | 8 * ((row >> 3) & 1); }
+
 // Epilogue of one wave's 128 x 128 tile whose accumulators hold transposed
 // 16 x 16 blocks (the MFMA computed B*A^T): lane l's acc[i][j][e] is tile
 // element (16i + l%16, 16j + 4*(l/16) + e), i.e. four adjacent columns.
@@ -264,6 +274,10 @@ gemm_nt_lds4k64_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
 // Preconditions: M % 256 == 0, N % 256 == 0, K % 64 == 0, beta == 0, C 16-byte
 // aligned, M*K*2 and N*K*2 below 2^32. Every store is then unconditional, which
 // keeps the per-wave count of outstanding vector-memory operations exact.
+// BNN: B is stored [K,N] (the NN GEMM of the IR's MATMUL and of the reference's
+// cutlass_gemm_tensorcore_bf16); its stages are 64 k-rows of 256 n and its
+// fragments come from transpose reads (nn_swz above). Same MFMA inputs in the
+// same order as the [N,K] form, so both give bit-identical C.
 // Implicit-GEMM view of an NHWC convolution for the persistent kernel: A row
 // m = output pixel (n, p, q), A column k = (r, s, c) with c fastest (the KRSC
 // filter is the NT B operand). With C % 64 == 0 one 64-deep K stage is 64
@@ -275,7 +289,7 @@ struct ConvGeomP {
     uint32_t x_bytes;
 };
 
-template <typename T, int GA, int GB, int EPI, bool CONV = false>
+template <typename T, int GA, int GB, int EPI, bool CONV = false, bool BNN = false>
 __global__ void __launch_bounds__(256, 1)
 gemm_nt_persist_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                        uint16_t* __restrict__ C, int M, int N, int K, float alpha,
@@ -340,7 +354,16 @@ gemm_nt_persist_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
             } else {
                 voff[j] = (uint32_t)(((size_t)(m0 + row) * K + lch * 8) * 2);
             }
-            voff[LOADS + j] = (uint32_t)(((size_t)(n0 + row) * K + lch * 8) * 2);
+            if constexpr (BNN) {
+                // DMA load j of B moves k-rows 2q, 2q+1 (q = 4j + wave) of the
+                // [64 k][256 n] stage; lane i: k-row 2q + i/32, physical chunk
+                // i%32 holding logical chunk (i%32) ^ nn_swz(k-row)
+                const int brow = 2 * (j * 4 + wave) + lane / 32;
+                const int bch = (lane % 32) ^ nn_swz(brow);
+                voff[LOADS + j] = (uint32_t)(((size_t)brow * N + n0 + bch * 8) * 2);
+            } else {
+                voff[LOADS + j] = (uint32_t)(((size_t)(n0 + row) * K + lch * 8) * 2);
+            }
         }
     };
 #pragma unroll
@@ -378,8 +401,9 @@ gemm_nt_persist_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
                    : 0xFFFFFFF0u;  // past the end of x: reads zeros
             lds_dma_buf_b128_u(a_rsrc, off, 0u, ldso[j] + (uint32_t)buf * STAGE_BYTES);
         } else {
-            lds_dma_buf_b128(j < LOADS ? a_rsrc : b_rsrc, voff[j], (uint32_t)(kt * BK * 2),
-                             ldso[j] + (uint32_t)buf * STAGE_BYTES);
+            // stage kt of B starts at k-row 64 kt ([K,N]) or at column 64 kt ([N,K])
+            const uint32_t soff = (BNN && j >= LOADS) ? (uint32_t)kt * (uint32_t)(BK * N * 2) : (uint32_t)(kt * BK * 2);
+            lds_dma_buf_b128(j < LOADS ? a_rsrc : b_rsrc, voff[j], soff, ldso[j] + (uint32_t)buf * STAGE_BYTES);
         }
     };
     auto issue_prologue = [&]() {
@@ -398,6 +422,29 @@ gemm_nt_persist_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
         a_rd[h] = As + (wm * 128 + lrow) * BK + pc * 8;
         b_rd[h] = Bs + (wn * 128 + lrow) * BK + pc * 8;
     }
+    // [K,N] B: fragment j of k-half h (n = wn*128 + 16j + lane%16, k = 32h +
+    // 8*(lane/16) + 0..7) by two transpose reads (k +0..3, +4..7). Lane L of
+    // 16-lane group g addresses k-row 32h + 8g + 4r + L/4, columns 16j +
+    // 4*(L%4) .. +3 of the wave's n range; the swizzle depends on the row only
+    // through L/4 and g, so it is one value per lane for every (h, r, j).
+    const int g16 = lane >> 4;
+    const int bsw = nn_swz(8 * g16 + (lrow >> 2));
+    const uint16_t* const b_nn = Bs + (8 * g16 + (lrow >> 2)) * 256 + wn * 128 + ((lrow & 3) >> 1) * 8 + (lrow & 1) * 4;
+    int b_jo[BNN ? 8 : 1];
+    if constexpr (BNN) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) b_jo[j] = ((2 * j) ^ bsw) * 8;
+    }
+    auto read_b = [&](int h, int j, uint32_t bufo) {
+        if constexpr (BNN) {
+            const uint16_t* p = b_nn + bufo + b_jo[j] + h * 32 * 256;
+            const u32x2 lo = lds_read_tr16(p);
+            const u32x2 hi = lds_read_tr16(p + 4 * 256);
+            return u32x4{lo[0], lo[1], hi[0], hi[1]};
+        } else {
+            return *reinterpret_cast<const u32x4*>(b_rd[h] + bufo + j * 16 * BK);
+        }
+    };
 
     f32x4 acc[8][8];
     u32x4 fa[2][8], fb[2][8];
@@ -420,7 +467,7 @@ gemm_nt_persist_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             fa[0][i] = *reinterpret_cast<const u32x4*>(a_rd[0] + i * 16 * BK);
-            fb[0][i] = *reinterpret_cast<const u32x4*>(b_rd[0] + i * 16 * BK);
+            fb[0][i] = read_b(0, i, 0);
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i)
@@ -456,7 +503,7 @@ gemm_nt_persist_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
                 if (g < 16) {
                     const int f = g >> 1;
                     if ((g & 1) == 0) fa[1][f] = *reinterpret_cast<const u32x4*>(a_rd[1] + cur + f * 16 * BK);
-                    else fb[1][f] = *reinterpret_cast<const u32x4*>(b_rd[1] + cur + f * 16 * BK);
+                    else fb[1][f] = read_b(1, f, cur);
                 }
                 if (g >= GA && g < GA + 16) dma(g - GA, dkt, dbuf, dtap);
                 if (g >= GB && g < GB + 16) {
@@ -464,7 +511,7 @@ gemm_nt_persist_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
                     if (((g - GB) & 1) == 0)
                         fa[0][f] = *reinterpret_cast<const u32x4*>(a_rd[0] + nxt + f * 16 * BK);
                     else
-                        fb[0][f] = *reinterpret_cast<const u32x4*>(b_rd[0] + nxt + f * 16 * BK);
+                        fb[0][f] = read_b(0, f, nxt);
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -594,6 +641,53 @@ extern "C" int pyc_hip_gemm_nt_lds_launch(int is_bf16, int M, int N, int K, cons
             hipLaunchKernelGGL((gemm_nt_lds4k64_kernel<f16_t, 24, 40>), grid, block, 0, s, a, b, c, M, N, K, alpha,
                                beta, bias, epi, tiles_m, tiles_n, 8);
     }
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+// NN form (B stored [K,N]) of the persistent kernel: returns 1 when the shape
+// is outside its preconditions (M, N multiples of 256, K of 64, beta == 0,
+// 16-byte aligned C and bias, M*K*2 and K*N*2 below 2^32, at least as many
+// 256 x 256 tiles as CUs), 0 on launch, -2 on a launch error.
+extern "C" int pyc_hip_gemm_nn_lds_launch(int is_bf16, int M, int N, int K, const void* A, const void* B,
+                                          void* C, float alpha, float beta, const float* bias, int epi,
+                                          void* stream) {
+    using namespace pyc;
+    if (M <= 0 || N <= 0 || K <= 0 || M % kD_BM != 0 || N % kD_BN != 0 || K % 64 != 0 || beta != 0.f) return 1;
+    if ((size_t)M * K * 2 > 0xFFFFFFFFull || (size_t)N * K * 2 > 0xFFFFFFFFull) return 1;
+    if (((uintptr_t)C & 15) != 0 || ((epi & 1) && bias != nullptr && ((uintptr_t)bias & 15) != 0)) return 1;
+    static int n_cu = 0;
+    if (n_cu == 0) {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
+            n_cu = cus;
+        else
+            n_cu = 256;
+    }
+    const int tiles_m = M / kD_BM, tiles_n = N / kD_BN;
+    const int ntiles = tiles_m * tiles_n;
+    if (ntiles < n_cu) return 1;  // fewer tiles than CUs: the 128 x 128 kernels fill the chip better
+    hipStream_t s = (hipStream_t)stream;
+    const int pepi = (((epi & 1) && bias != nullptr) ? 1 : 0) | (epi & 2);
+    const dim3 grid(n_cu), block(4 * kWave);
+    const uint16_t* a = (const uint16_t*)A;
+    const uint16_t* b = (const uint16_t*)B;
+    uint16_t* c = (uint16_t*)C;
+#define PYC_PERSIST_NN(TY, E) \
+    hipLaunchKernelGGL((gemm_nt_persist_kernel<TY, 24, 40, E, false, true>), grid, block, 0, s, a, b, c, M, N, K, \
+                       alpha, bias, tiles_m, tiles_n, 8)
+    if (is_bf16) {
+        if (pepi == 0) PYC_PERSIST_NN(bf16_t, 0);
+        else if (pepi == 1) PYC_PERSIST_NN(bf16_t, 1);
+        else if (pepi == 2) PYC_PERSIST_NN(bf16_t, 2);
+        else PYC_PERSIST_NN(bf16_t, 3);
+    } else {
+        if (pepi == 0) PYC_PERSIST_NN(f16_t, 0);
+        else if (pepi == 1) PYC_PERSIST_NN(f16_t, 1);
+        else if (pepi == 2) PYC_PERSIST_NN(f16_t, 2);
+        else PYC_PERSIST_NN(f16_t, 3);
+    }
+#undef PYC_PERSIST_NN
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 

@@ -56,6 +56,19 @@ __device__ inline i32x4 make_buf_rsrc(const void* base, uint32_t bytes) {
     return r;
 }
 
+// LDS transpose read (gfx950 ds_read_b64_tr_b16): within each group of 16
+// lanes, lane i receives element (i & 3) of the 8 bytes that lane
+// 4j + (i >> 2) addresses, as its element j. A group whose lane L addresses
+// row (r0 + L/4), columns (c0 + 4*(L%4)) .. +3 of a row-major 16-bit tile
+// therefore gets, in lane i, rows r0..r0+3 of column c0 + i: a column-major
+// MFMA operand read from a row-major tile.
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+__device__ inline u32x2 lds_read_tr16(const uint16_t* p) {
+    const v4i16_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) v4i16_t*)(__attribute__((address_space(3))) uint16_t*)p);
+    return __builtin_bit_cast(u32x2, v);
+}
+
 template <int N> __device__ inline void wait_vmem_le() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }

@@ -45,9 +45,17 @@ SHAPES = [(256, 256, 64), (512, 768, 256), (300, 200, 72), (1, 1, 8), (33, 65, 4
 @pytest.mark.parametrize("tile", ["", "_128x128", "_256x256", "_256x256_lds"])
 def test_bf16_gemm_vs_oracle(gpu, m, n, k, layout, tile):
     torch = gpu
-    if tile.endswith("lds") and layout == "nn":
-        pytest.skip("the direct-LDS kernel is NT only")
     bt = layout == "nt"
+    if tile.endswith("lds") and layout == "nn" and not (m % 256 == 0 and n % 256 == 0 and k % 64 == 0 and
+                                                        (m // 256) * (n // 256) >= 256):
+        # the NN persistent kernel alone: shapes outside it are refused, nothing launched
+        a, b = _bf16_inputs(m, n, k, 1, bt)
+        A, B = dev_bits16(torch, a), dev_bits16(torch, b)
+        Cd = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+        rc = pyc_amd.lib().pyc_hip_gemm_dispatch(b"hip_gemm_bf16_nn_256x256_lds", m, n, k, A.data_ptr(),
+                                                 B.data_ptr(), Cd.data_ptr(), 1.0, 0.0, None, 0, None)
+        assert rc == -1
+        return
     a, b = _bf16_inputs(m, n, k, m * 7 + n + k, bt)
     A, B = dev_bits16(torch, a), dev_bits16(torch, b)
     Cd = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
@@ -216,3 +224,79 @@ def test_reference_symbols_and_rejections(gpu):
                                        B.data_ptr(), Cd.data_ptr(), 1.0, 1.0, s) == -1
     assert L.pyc_hip_gemm_dispatch(b"hip_gemm_bf16_nt", 0, n, k, A.data_ptr(), B.data_ptr(),
                                    Cd.data_ptr(), 1.0, 0.0, None, 0, s) == -1
+
+
+@pytest.mark.parametrize("m,n,k", [(4096, 4096, 512), (17 * 256, 17 * 256, 128), (8192, 4096, 1024)])
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_nn_lds_equals_nt_on_transpose(gpu, m, n, k, dtype):
+    """The persistent kernel with a [K,N] operand (transpose reads from LDS)
+    feeds the MFMAs the same values in the same order as the [N,K] form, so
+    C = A B equals the NT kernel's A (B^T)^T bit for bit; the NT kernel is
+    itself checked against the oracle above."""
+    torch = gpu
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    g = torch.Generator(device="cuda").manual_seed(m + n + k)
+    A = (torch.randn((m, k), generator=g, device="cuda") / np.sqrt(k)).to(tdt)
+    B = torch.randn((k, n), generator=g, device="cuda").to(tdt)
+    Bt = B.t().contiguous()
+    Cn = torch.empty((m, n), dtype=tdt, device="cuda")
+    Ct = torch.empty_like(Cn)
+    pyc_amd.gemm(f"hip_gemm_{dtype}_nn_256x256_lds", A, B, Cn, m, n, k)
+    pyc_amd.gemm(f"hip_gemm_{dtype}_nt_256x256_lds", A, Bt, Ct, m, n, k)
+    torch.cuda.synchronize()
+    assert torch.equal(Cn.view(torch.int16), Ct.view(torch.int16))
+
+
+@pytest.mark.parametrize("alpha,epi", [(0.5, 3), (1.0, 2), (-2.0, 1)])
+def test_nn_lds_epilogues(gpu, alpha, epi):
+    """Bias / ReLU / alpha through the NN persistent kernel equal the NT
+    kernel's on the transposed operand, and the oracle's to the bf16 bar."""
+    torch = gpu
+    m = n = 4096
+    k = 256
+    r = np.random.default_rng(epi)
+    a, b = _bf16_inputs(m, n, k, 40 + epi, False)
+    bias = r.standard_normal(n).astype(np.float32)
+    A, B = dev_bits16(torch, a), dev_bits16(torch, b)
+    Bt = B.t().contiguous()
+    Bv = dev_f32(torch, bias)
+    Cn = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    Ct = torch.empty_like(Cn)
+    pyc_amd.gemm("hip_gemm_bf16_nn", A, B, Cn, m, n, k, alpha=alpha, bias=Bv, epilogue=epi)
+    pyc_amd.gemm("hip_gemm_bf16_nt", A, Bt, Ct, m, n, k, alpha=alpha, bias=Bv, epilogue=epi)
+    torch.cuda.synchronize()
+    assert torch.equal(Cn.view(torch.int16), Ct.view(torch.int16))
+    rows = np.arange(0, m, 61)
+    ref = alpha * oracle.gemm_bf16(a[rows], b, False, threads=8)
+    if epi & 1:
+        ref = ref + bias[None, :]
+    if epi & 2:
+        ref = np.maximum(ref, 0)
+    got = oracle.bf16_to_f32(host_bits16(Cn[torch.from_numpy(rows).cuda()]))
+    assert rel_max_err(got, ref) <= BF16_TOL
+
+
+def test_reference_bf16_symbol_8192_row_major_b(gpu):
+    """The reference's default bf16 symbol (cutlass_gemm_tensorcore_bf16, B
+    row-major [K,N], reference gemm/kernel.cu:175-187) at config 2's size: it
+    runs the NN persistent kernel; rows sampled over every tile row against the
+    oracle, plus the column-sum property on all of C."""
+    torch = gpu
+    m = n = k = 8192
+    g = torch.Generator(device="cuda").manual_seed(1)
+    A = (torch.randn((m, k), generator=g, device="cuda") / np.sqrt(k)).to(torch.bfloat16)
+    g2 = torch.Generator(device="cuda").manual_seed(2)
+    B = (torch.randn((k, n), generator=g2, device="cuda") / np.sqrt(k)).to(torch.bfloat16)
+    Cd = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    L = pyc_amd.lib()
+    assert L.pyc_cutlass_gemm_dispatch(b"cutlass_gemm_tensorcore_bf16", m, n, k, A.data_ptr(), B.data_ptr(),
+                                       Cd.data_ptr(), 1.0, 0.0, None) == 0
+    torch.cuda.synchronize()
+    rows = np.unique(np.concatenate([np.arange(0, m, 263), [m - 1]]))
+    a = host_bits16(A[torch.from_numpy(rows).cuda()])
+    b = host_bits16(B)
+    ref = oracle.gemm_bf16(a, b, False, threads=16)
+    _check_half(host_bits16(Cd[torch.from_numpy(rows).cuda()]), ref, k)
+    colsum = Cd.float().sum(0).double()
+    pred = (A.double().sum(0, keepdim=True) @ B.double()).squeeze(0)
+    assert (colsum - pred).abs().max().item() <= 1e-2 * pred.abs().max().item()
