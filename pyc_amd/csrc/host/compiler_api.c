@@ -127,6 +127,18 @@ struct pyc_compiled_model {
     float* workspace[PYC_IR_MAX_OPS];
     size_t workspace_bytes[PYC_IR_MAX_OPS];
     char log[LOG_MAX];
+    /* the last run's decision-log inputs: the text is formatted when it is
+     * read (pyc_model_last_decision_log), not on every run; only
+     * pyc_run_model changes a model, so the fields it reads are the run's */
+    struct {
+        int pending;
+        pyc_alloc_stats st;
+        pyc_kernel_workload_family wl;
+        pyc_kernel_hardware_family hw;
+        int contract_ok, spec_hit, phantom_hit;
+        char contract_why[64];
+        char bucket[64];
+    } runlog;
 };
 
 /* ---------------------------------------------------------------- small helpers */
@@ -1412,6 +1424,7 @@ static void compile_log(pyc_compiled_model* model) {
     const pyc_pass_report* r = &a->report;
     logbuf lb = {model->log, sizeof(model->log), 0};
     model->log[0] = '\0';
+    model->runlog.pending = 0;
     logf_(&lb, "mode=%d budget=%zu pressure=%.6f kernel=%s score=%.3f util=%.3f alloc_penalty=%.3f "
                "reuse_bonus=%.3f kernel_candidates=%zu det=%d cache_hit=%d compile_ms=%.3f budget_ms=%.3f "
                "budget_exceeded=%d graph_breaks=%zu break_first=%s@%d break_counts=%zu,%zu,%zu,%zu,%zu "
@@ -1547,17 +1560,39 @@ pyc_status pyc_compile_model(const pyc_model_desc* desc, const pyc_compile_optio
 
 /* ---------------------------------------------------------------- run */
 
+/* Records the run's decision-log inputs; run_log_format writes the text. */
 static void run_log(pyc_compiled_model* model, const pyc_alloc_stats* st, pyc_kernel_workload_family wl,
                     pyc_kernel_hardware_family hw, int contract_ok, const char* contract_why, int spec_hit,
                     int phantom_hit, const char* bucket) {
+    model->log[0] = '\0';
+    model->runlog.pending = env_on_default("PYC_ENABLE_RUNTIME_DECISION_LOG");
+    if (!model->runlog.pending) {
+        return;
+    }
+    model->runlog.st = *st;
+    model->runlog.wl = wl;
+    model->runlog.hw = hw;
+    model->runlog.contract_ok = contract_ok;
+    model->runlog.spec_hit = spec_hit;
+    model->runlog.phantom_hit = phantom_hit;
+    copy_str(model->runlog.contract_why, sizeof(model->runlog.contract_why), contract_why);
+    copy_str(model->runlog.bucket, sizeof(model->runlog.bucket), bucket);
+}
+
+static void run_log_format(pyc_compiled_model* model) {
     const compiled_artifacts* a = &model->art;
     const pyc_pass_report* r = &a->report;
     const phantom_state* ph = &a->phantom;
+    const pyc_alloc_stats* st = &model->runlog.st;
+    const pyc_kernel_workload_family wl = model->runlog.wl;
+    const pyc_kernel_hardware_family hw = model->runlog.hw;
+    const int contract_ok = model->runlog.contract_ok, spec_hit = model->runlog.spec_hit;
+    const int phantom_hit = model->runlog.phantom_hit;
+    const char* contract_why = model->runlog.contract_why;
+    const char* bucket = model->runlog.bucket;
     logbuf lb = {model->log, sizeof(model->log), 0};
     model->log[0] = '\0';
-    if (!env_on_default("PYC_ENABLE_RUNTIME_DECISION_LOG")) {
-        return;
-    }
+    model->runlog.pending = 0;
     logf_(&lb, "mode=%d shadow_mode=%d shadow_reason=%d rollback=%d rollback_count=%zu pressure=%.6f kernel=%s "
                "score=%.3f util=%.3f alloc_penalty=%.3f reuse_bonus=%.3f kernel_candidates=%zu workload=%s hw=%s ",
           (int)model->options.objective_mode, (int)model->controller.recommended_mode,
@@ -1871,7 +1906,13 @@ pyc_status pyc_run_model(pyc_compiled_model* model, const pyc_tensor* inputs, si
 }
 
 const char* pyc_model_last_decision_log(const pyc_compiled_model* model) {
-    return model ? model->log : "";
+    if (!model) {
+        return "";
+    }
+    if (model->runlog.pending) {
+        run_log_format((pyc_compiled_model*)model); /* the handle is the caller's mutable model */
+    }
+    return model->log;
 }
 
 const pyc_collective_comm* pyc_model_distributed_comm(const pyc_compiled_model* model) {

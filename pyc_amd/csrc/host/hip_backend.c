@@ -724,6 +724,19 @@ typedef struct {
     size_t cap;
 } hbuf;
 
+/* Executable graphs kept for replay. A process that alternates models (a
+ * prefill and a decode module, say) replays each one's graph instead of
+ * re-capturing on every switch. */
+#define GRAPH_SLOTS 8
+
+typedef struct {
+    int valid;
+    uint64_t sig;
+    uint64_t last_use;
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+} graph_slot;
+
 static struct {
     int ready;
     int device;
@@ -737,20 +750,57 @@ static struct {
     size_t last_bytes[PYC_IR_MAX_OPS];
     int uploaded[PYC_IR_MAX_OPS];
     int* chain_err;                /* pinned copy of the chain kernel's timeout word */
-    /* graph replay */
-    hipGraphExec_t gexec;
-    hipGraph_t graph;
-    int graph_valid;
-    uint64_t graph_sig;
+    uint64_t upload_module;        /* module whose static inputs val[] holds (uploaded[]) */
+    /* graph replay: one executable graph per run signature, least recently
+     * used one replaced */
+    graph_slot graphs[GRAPH_SLOTS];
+    uint64_t graph_clock;
 } g_ws;
+
+/* Destroys every cached graph: they bake in workspace addresses, so a buffer
+ * that moves (or is released) invalidates all of them. */
+static void graphs_flush(void) {
+    size_t i;
+    for (i = 0; i < GRAPH_SLOTS; ++i) {
+        if (g_ws.graphs[i].valid) {
+            (void)hipGraphExecDestroy(g_ws.graphs[i].exec);
+            (void)hipGraphDestroy(g_ws.graphs[i].graph);
+            g_ws.graphs[i].valid = 0;
+        }
+    }
+}
+
+static graph_slot* graph_find(uint64_t sig) {
+    size_t i;
+    for (i = 0; i < GRAPH_SLOTS; ++i) {
+        if (g_ws.graphs[i].valid && g_ws.graphs[i].sig == sig) {
+            g_ws.graphs[i].last_use = ++g_ws.graph_clock;
+            return &g_ws.graphs[i];
+        }
+    }
+    return NULL;
+}
+
+/* A free slot, else the least recently used one (its graph destroyed). */
+static graph_slot* graph_victim(void) {
+    size_t i, v = 0;
+    for (i = 0; i < GRAPH_SLOTS; ++i) {
+        if (!g_ws.graphs[i].valid) {
+            return &g_ws.graphs[i];
+        }
+        if (g_ws.graphs[i].last_use < g_ws.graphs[v].last_use) {
+            v = i;
+        }
+    }
+    (void)hipGraphExecDestroy(g_ws.graphs[v].exec);
+    (void)hipGraphDestroy(g_ws.graphs[v].graph);
+    g_ws.graphs[v].valid = 0;
+    return &g_ws.graphs[v];
+}
 
 static void ws_release(void) {
     size_t i;
-    if (g_ws.graph_valid) {
-        (void)hipGraphExecDestroy(g_ws.gexec);
-        (void)hipGraphDestroy(g_ws.graph);
-        g_ws.graph_valid = 0;
-    }
+    graphs_flush();
     for (i = 0; i < PYC_IR_MAX_OPS; ++i) {
         if (g_ws.val[i].ptr) {
             (void)hipFree(g_ws.val[i].ptr);
@@ -801,16 +851,12 @@ static int ws_init(void) {
     return 0;
 }
 
-/* Grow-only device buffer; growth invalidates a captured graph. */
+/* Grow-only device buffer; growth invalidates the captured graphs. */
 static int dgrow(dbuf* b, size_t bytes) {
     if (b->cap >= bytes && b->ptr) {
         return 0;
     }
-    if (g_ws.graph_valid) {
-        (void)hipGraphExecDestroy(g_ws.gexec);
-        (void)hipGraphDestroy(g_ws.graph);
-        g_ws.graph_valid = 0;
-    }
+    graphs_flush();
     if (b->ptr) {
         (void)hipFree(b->ptr);
         b->ptr = NULL;
@@ -828,11 +874,7 @@ static int hgrow(hbuf* b, size_t bytes) {
     if (b->cap >= bytes && b->ptr) {
         return 0;
     }
-    if (g_ws.graph_valid) {
-        (void)hipGraphExecDestroy(g_ws.gexec);
-        (void)hipGraphDestroy(g_ws.graph);
-        g_ws.graph_valid = 0;
-    }
+    graphs_flush();
     if (b->ptr) {
         (void)hipHostFree(b->ptr);
         b->ptr = NULL;
@@ -914,12 +956,20 @@ static int any_device_tensor(const pyc_tensor* inputs, size_t input_count, const
     return 0;
 }
 
+/* Run-signature hash: FNV-1a's multiply over 8-byte words (then the tail
+ * bytes), with a shift-xor so high bits reach the low ones. Only equality of
+ * two signatures matters; it runs on every call, so it takes words. */
 static uint64_t fnv(uint64_t h, const void* p, size_t n) {
     const unsigned char* c = (const unsigned char*)p;
-    size_t i;
-    for (i = 0; i < n; ++i) {
-        h ^= c[i];
-        h *= 1099511628211ull;
+    size_t i = 0;
+    for (; i + 8 <= n; i += 8) {
+        uint64_t w;
+        memcpy(&w, c + i, sizeof(w));
+        h = (h ^ w) * 1099511628211ull;
+        h ^= h >> 29;
+    }
+    for (; i < n; ++i) {
+        h = (h ^ c[i]) * 1099511628211ull;
     }
     return h;
 }
@@ -1026,7 +1076,7 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
     const int static_lhs = env_true("PYC_CUDA_ASSUME_STATIC_LHS");
     const int static_rhs = env_true("PYC_CUDA_ASSUME_STATIC_RHS");
     const int skip_out = env_true("PYC_CUDA_SKIP_HOST_OUTPUT_COPY");
-    const int use_graph = env_default_true("PYC_CUDA_ENABLE_GRAPH_REPLAY");
+    int use_graph = env_default_true("PYC_CUDA_ENABLE_GRAPH_REPLAY");
     int copy_in[PYC_IR_MAX_OPS];
     void* vp[PYC_IR_MAX_OPS];   /* device storage of each value: workspace or the caller's device tensor */
     int dev_in[PYC_IR_MAX_OPS]; /* INPUT op bound to the caller's device tensor (no staging, no copy) */
@@ -1035,7 +1085,8 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
     int any_dev = 0;
     int has_chain = 0;
     size_t i;
-    uint64_t sig = 1469598103934665603ull;
+    uint64_t sig = 1469598103934665603ull, mod_sig;
+    graph_slot* gs = NULL;
     int replayed = 0;
     double t0;
     float dev_ms = 0.0f;
@@ -1051,6 +1102,15 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
     if (ws_init() != 0) {
         snprintf(why, why_cap, "hip_workspace_init_failed");
         return -1;
+    }
+
+    /* static-input uploads (uploaded[]) stay valid only while the same module
+     * runs: another module's values share the per-op-id device buffers */
+    mod_sig = fnv(sig, &m->op_count, sizeof(m->op_count));
+    mod_sig = fnv(mod_sig, m->ops, m->op_count * sizeof(pyc_ir_op));
+    if (g_ws.upload_module != mod_sig) {
+        memset(g_ws.uploaded, 0, sizeof(g_ws.uploaded));
+        g_ws.upload_module = mod_sig;
     }
 
     /* bind inputs, size checks, device + staging buffers */
@@ -1202,9 +1262,21 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
         }
     }
 
-    /* run signature: module content + host pointers + copy flags */
-    sig = fnv(sig, &m->op_count, sizeof(m->op_count));
-    sig = fnv(sig, m->ops, m->op_count * sizeof(pyc_ir_op));
+    /* A plan that records one operation (one kernel step, no copies) is
+     * launched directly: a graph of one node only adds launch latency. */
+    if (use_graph && !has_chain) {
+        size_t nodes = plan.nsteps;
+        for (i = 0; i < m->op_count; ++i) {
+            nodes += plan.input_ordinal[i] >= 0 && copy_in[i];
+        }
+        for (i = 0; i < plan.n_outputs; ++i) {
+            nodes += dev_out[i] ? (size_t)out_d2d[i] : (size_t)!skip_out;
+        }
+        use_graph = nodes >= 2;
+    }
+
+    /* run signature: module content + device pointers + copy flags */
+    sig = mod_sig;
     sig = fnv(sig, &skip_out, sizeof(skip_out));
     sig = fnv(sig, &g_tune_gen, sizeof(g_tune_gen));
     /* the planned kernels: an env or registry change of a symbol recaptures */
@@ -1220,7 +1292,7 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
         }
     }
     /* a graph bakes in the caller's device tensors: their addresses are part of the run */
-    sig = fnv(sig, vp, sizeof(vp));
+    sig = fnv(sig, vp, m->op_count * sizeof(vp[0]));
     for (i = 0; i < plan.n_outputs; ++i) {
         sig = fnv(sig, &dev_out[i], sizeof(int));
         if (dev_out[i]) {
@@ -1240,16 +1312,12 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
         trace->copy_in_ms += now_ms() - t0;
     }
 
-    if (use_graph && g_ws.graph_valid && g_ws.graph_sig == sig) {
+    gs = use_graph ? graph_find(sig) : NULL;
+    if (gs) {
         replayed = 1;
     } else {
-        /* (re)record: either into a graph or directly */
+        /* record: either into a new graph or directly */
         hipError_t cerr = hipSuccess;
-        if (g_ws.graph_valid) {
-            (void)hipGraphExecDestroy(g_ws.gexec);
-            (void)hipGraphDestroy(g_ws.graph);
-            g_ws.graph_valid = 0;
-        }
         if (use_graph) {
             /* the fp8 GEMM's split-K workspace cannot be allocated inside a capture */
             for (i = 0; i < plan.nsteps; ++i) {
@@ -1305,12 +1373,16 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
             }
             if (use_graph) {
                 hipGraph_t graph = NULL;
+                hipGraphExec_t exec = NULL;
                 hipError_t e = hipStreamEndCapture(g_ws.stream, &graph);
                 if (rc == 0 && e == hipSuccess && graph &&
-                    hipGraphInstantiate(&g_ws.gexec, graph, NULL, NULL, 0) == hipSuccess) {
-                    g_ws.graph = graph;
-                    g_ws.graph_valid = 1;
-                    g_ws.graph_sig = sig;
+                    hipGraphInstantiate(&exec, graph, NULL, NULL, 0) == hipSuccess) {
+                    gs = graph_victim();
+                    gs->graph = graph;
+                    gs->exec = exec;
+                    gs->sig = sig;
+                    gs->last_use = ++g_ws.graph_clock;
+                    gs->valid = 1;
                 } else {
                     if (graph) {
                         (void)hipGraphDestroy(graph);
@@ -1335,7 +1407,7 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
     t0 = now_ms();
     if (use_graph) {
         if (hipEventRecord(g_ws.ev0, g_ws.stream) != hipSuccess ||
-            hipGraphLaunch(g_ws.gexec, g_ws.stream) != hipSuccess ||
+            hipGraphLaunch(gs->exec, g_ws.stream) != hipSuccess ||
             hipEventRecord(g_ws.ev1, g_ws.stream) != hipSuccess) {
             snprintf(why, why_cap, "hip_graph_launch_failed");
             return -1;

@@ -9,26 +9,32 @@
 // the row-bias + ReLU epilogue the reference ran on the host after the copy
 // back (reference cuda_backend.c:1697-1742).
 //
-// Tile 64x64x64, 4 waves (2x2) of 32x32; each lane reads 4 consecutive k of
-// its row as one 16-byte LDS load and issues 4 MFMAs, one per element, so A
-// and B use the same k permutation {4*(lane/16)+e}. B is staged in LDS as
-// [n][k] for both layouts ([K,N] tiles are transposed on the LDS store).
+// Tile 64x64x64, 8 waves: waves 0-3 and 4-7 each cover the tile as 2x2 of
+// 32x32, the first four on k 0-31 and the second four on k 32-63 of every
+// k-tile; the two halves are added through LDS at the end (fixed order). Two
+// waves per SIMD let one wave's MFMAs run while the other waits at the
+// barrier or on LDS, which one wave per SIMD (one 64x64 tile per CU at
+// 1024^3) could not hide. Each lane reads 4 consecutive k of its row as one
+// 16-byte LDS load and issues 4 MFMAs, one per element, so A and B use the
+// same k permutation {4*(lane/16)+e}. B is staged in LDS as [n][k] for both
+// layouts ([K,N] tiles are transposed on the LDS store). Waves 0-3 stage B,
+// waves 4-7 stage A.
 #include "common.hpp"
 
 namespace pyc {
 
 constexpr int kF32BM = 64;
 constexpr int kF32BN = 64;
-// K depth 64: one tile's MFMAs (about 1 us at 1024^3, one workgroup per CU)
-// cover the global loads of the next tile, which depth 32 did not
+// K depth 64: one tile's MFMAs cover the global loads of the next tile,
+// which depth 32 did not
 constexpr int kF32BK = 64;
 constexpr int kF32Ch = kF32BK / 4;  // 16-byte chunks per LDS row (16)
-constexpr int kF32Ld = kF32BM * kF32Ch / 256;  // 16-byte loads per thread per operand tile (4)
+constexpr int kF32Ld = kF32BM * kF32Ch / 256;  // 16-byte loads per staging thread (4)
 
 __device__ inline int swz8(int row, int chunk) { return chunk ^ (row & 7); }
 
 template <bool BT, bool GUARD>
-__global__ void __launch_bounds__(256, 2)
+__global__ void __launch_bounds__(512, 2)
 gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,
                 int M, int N, int K, float alpha, float beta, const float* __restrict__ bias,
                 int epi) {
@@ -38,15 +44,19 @@ gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ B, float*
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int wm = wave >> 1;
-    const int wn = wave & 1;
+    const int quad = wave & 3;
+    const int kh = wave >> 2;      // k half of every k-tile this wave multiplies
+    const int wm = quad >> 1;
+    const int wn = quad & 1;
+    const bool stage_a = kh != 0;  // waves 4-7 stage A, waves 0-3 stage B
+    const int t = tid & 255;
     const int m0 = blockIdx.y * kF32BM;
     const int n0 = blockIdx.x * kF32BN;
     const bool vec_k = (K & 3) == 0;
     const bool vec_n = (N & 3) == 0;
 
-    // 64 rows x 16 chunks = 1024 chunks per operand tile -> 4 per thread.
-    f32x4 ra[kF32Ld], rb[kF32Ld];
+    // 64 rows x 16 chunks = 1024 chunks per operand tile -> 4 per staging thread.
+    f32x4 rg[kF32Ld];
 
     auto ld4 = [&](const float* base, int r, int rmax, int c, int cmax, bool vec, size_t ld) -> f32x4 {
         if (!GUARD) return *reinterpret_cast<const f32x4*>(base + (size_t)r * ld + c);
@@ -59,36 +69,38 @@ gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ B, float*
     auto load = [&](int k0) {
 #pragma unroll
         for (int i = 0; i < kF32Ld; ++i) {
-            const int q = tid + i * 256;
+            const int q = t + i * 256;
             const int row = q / kF32Ch, ch = q % kF32Ch;
-            ra[i] = ld4(A, m0 + row, M, k0 + ch * 4, K, vec_k, (size_t)K);
-            if (BT) {
-                rb[i] = ld4(B, n0 + row, N, k0 + ch * 4, K, vec_k, (size_t)K);
+            if (stage_a) {
+                rg[i] = ld4(A, m0 + row, M, k0 + ch * 4, K, vec_k, (size_t)K);
+            } else if (BT) {
+                rg[i] = ld4(B, n0 + row, N, k0 + ch * 4, K, vec_k, (size_t)K);
             } else {
-                // [K,N] tile: thread tid holds the 4 x 4 block of k rows
-                // 4*(tid/16) + i and columns 4*(tid%16) .. +3 (16 threads
-                // read one whole 256-byte row segment)
-                rb[i] = ld4(B, k0 + 4 * (tid >> 4) + i, K, n0 + 4 * (tid & 15), N, vec_n, (size_t)N);
+                // [K,N] tile: thread t holds the 4 x 4 block of k rows
+                // 4*(t/16) + i and columns 4*(t%16) .. +3 (16 threads read
+                // one whole 256-byte row segment)
+                rg[i] = ld4(B, k0 + 4 * (t >> 4) + i, K, n0 + 4 * (t & 15), N, vec_n, (size_t)N);
             }
         }
     };
     auto store = [&](int buf) {
+        if (stage_a || BT) {
+            float* dst = stage_a ? As[buf] : Bs[buf];
 #pragma unroll
-        for (int i = 0; i < kF32Ld; ++i) {
-            const int q = tid + i * 256;
-            const int row = q / kF32Ch, ch = q % kF32Ch;
-            *reinterpret_cast<f32x4*>(&As[buf][row * kF32BK + swz8(row, ch) * 4]) = ra[i];
-            if (BT) *reinterpret_cast<f32x4*>(&Bs[buf][row * kF32BK + swz8(row, ch) * 4]) = rb[i];
-        }
-        if (!BT) {
+            for (int i = 0; i < kF32Ld; ++i) {
+                const int q = t + i * 256;
+                const int row = q / kF32Ch, ch = q % kF32Ch;
+                *reinterpret_cast<f32x4*>(&dst[row * kF32BK + swz8(row, ch) * 4]) = rg[i];
+            }
+        } else {
             // the 4 x 4 block transposed in registers: column j of it is the
-            // 16-byte chunk tid/16 (k = 4*(tid/16) .. +3) of LDS row n
-            const int kc = tid >> 4;
+            // 16-byte chunk t/16 (k = 4*(t/16) .. +3) of LDS row n
+            const int kc = t >> 4;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int n = 4 * (tid & 15) + j;
+                const int n = 4 * (t & 15) + j;
                 *reinterpret_cast<f32x4*>(&Bs[buf][n * kF32BK + swz8(n, kc) * 4]) =
-                    f32x4{rb[0][j], rb[1][j], rb[2][j], rb[3][j]};
+                    f32x4{rg[0][j], rg[1][j], rg[2][j], rg[3][j]};
             }
         }
     };
@@ -109,8 +121,8 @@ gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ B, float*
         const bool more = kt + 1 < ktiles;
         if (more) load((kt + 1) * kF32BK);
 #pragma unroll
-        for (int kb = 0; kb < kF32BK / 16; ++kb) {
-            const int ch = kb * 4 + lgrp;
+        for (int kk = 0; kk < kF32BK / 32; ++kk) {
+            const int ch = (kh * 2 + kk) * 4 + lgrp;
             f32x4 af[2], bfr[2];
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
@@ -130,6 +142,27 @@ gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ B, float*
         if (more) store(buf ^ 1);
         __syncthreads();
     }
+
+    // k halves: waves 4-7 hand their sums to waves 0-3 through As[0] (free
+    // after the loop's last barrier); [quad][element][lane] keeps each store
+    // and load one contiguous 256-byte row per wave
+    float* red = As[0];
+    if (kh) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) red[(quad * 16 + (i * 2 + j) * 4 + r) * 64 + lane] = acc[i][j][r];
+    }
+    __syncthreads();
+    if (kh) return;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[i][j][r] += red[(quad * 16 + (i * 2 + j) * 4 + r) * 64 + lane];
 
     const bool has_bias = (epi & 1) && bias != nullptr;
     const bool relu = (epi & 2) != 0;
@@ -161,7 +194,7 @@ extern "C" int pyc_hip_gemm_f32_launch(int b_trans, int M, int N, int K, const v
                                        const void* B, void* C, float alpha, float beta,
                                        const float* bias, int epi, void* stream) {
     using namespace pyc;
-    dim3 grid((N + kF32BN - 1) / kF32BN, (M + kF32BM - 1) / kF32BM), block(256);
+    dim3 grid((N + kF32BN - 1) / kF32BN, (M + kF32BM - 1) / kF32BM), block(512);
     const bool even = (M % kF32BM == 0) && (N % kF32BN == 0) && (K % kF32BK == 0);
     hipStream_t s = (hipStream_t)stream;
     const float* a = (const float*)A;

@@ -103,6 +103,20 @@ class Model:
         rc = self.L.pyc_run_model(self.handle, ins, len(inputs), outs, len(outputs), C.byref(stats))
         return rc, stats
 
+    def bind(self, inputs, outputs):
+        """pyc_run_model on fixed tensor lists, with the argument arrays built
+        once: returns a function that runs the model and returns
+        (status, RunStats), as run() does."""
+        ins = (abi.Tensor * len(inputs))(*inputs)
+        outs = (abi.Tensor * len(outputs))(*outputs)
+        n_in, n_out, fn, h = len(inputs), len(outputs), self.L.pyc_run_model, self.handle
+
+        def call():
+            stats = abi.RunStats()
+            return fn(h, ins, n_in, outs, n_out, C.byref(stats)), stats
+
+        return call
+
     def decision_log(self) -> str:
         return self.L.pyc_model_last_decision_log(self.handle).decode()
 

@@ -56,6 +56,43 @@ def test_config1_through_run_model(monkeypatch):
     assert "hip_gemm_f32" in paths[0]
 
 
+def test_graph_cache_two_models_alternating():
+    """Two compiled models run in turn (a prefill and a decode module, say):
+    each keeps its own captured graph, so once both are captured every call
+    replays instead of re-capturing the other's graph away; results equal the
+    oracle on every call."""
+    r = np.random.default_rng(7)
+    x = r.uniform(-1, 1, (256, 192)).astype(np.float32)
+    w = r.uniform(-1, 1, (192, 128)).astype(np.float32)
+    b = r.uniform(-1, 1, 128).astype(np.float32)
+    ops_a = [eu.op(abi.OP_INPUT, "x", (256, 192)), eu.op(abi.OP_INPUT, "w", (192, 128)),
+             eu.op(abi.OP_INPUT, "bias", (128,)), eu.op(abi.OP_MATMUL, "matmul0", (), (0, 1)),
+             eu.op(abi.OP_ADD, "add0", (), (3, 2)), eu.op(abi.OP_RELU, "relu0", (), (4,)),
+             eu.op(abi.OP_OUTPUT, "out0", (256, 128), (5,))]
+    w2 = r.uniform(-1, 1, (128, 64)).astype(np.float32)
+    ops_b = [eu.op(abi.OP_INPUT, "x", (256, 192)), eu.op(abi.OP_INPUT, "w1", (192, 128)),
+             eu.op(abi.OP_INPUT, "b1", (128,)), eu.op(abi.OP_INPUT, "w2", (128, 64)),
+             eu.op(abi.OP_MATMUL, "mm1", (), (0, 1)), eu.op(abi.OP_ADD, "add1", (), (4, 2)),
+             eu.op(abi.OP_RELU, "relu1", (), (5,)), eu.op(abi.OP_MATMUL, "mm2", (), (6, 3)),
+             eu.op(abi.OP_OUTPUT, "o", (256, 64), (7,))]
+    ma = eu.Model(eu.mine(), ops_a, backend=abi.BACKEND_CUDA)
+    mb = eu.Model(eu.mine(), ops_b, backend=abi.BACKEND_CUDA)
+    assert ma.status == 0 and mb.status == 0
+    h = oracle.gemm_bias_relu_f32(x, w, b, relu=True)
+    ref_b = oracle.matmul_f32(h, w2)
+    pa, pb = [], []
+    for _ in range(4):
+        st, (out,), s = ma.run([x, w, b], [(256, 128)])
+        assert st == 0 and rel_max_err(out, h) <= 1e-4
+        pa.append(_native(s))
+        st, (out,), s = mb.run([x, w, b, w2], [(256, 64)])
+        assert st == 0 and rel_max_err(out, ref_b) <= 1e-4
+        pb.append(_native(s))
+    ma.close()
+    mb.close()
+    assert all("graph_replay" in p for p in pa[2:] + pb[2:]), (pa, pb)
+
+
 def test_bf16_matmul_module_nn():
     m, k, n = 320, 256, 192
     r = np.random.default_rng(1)

@@ -58,7 +58,7 @@ def _gemm_module(M, K, N, dtype=abi.DTYPE_F32, bias_dtype=None):
 
 def test_device_tensors_f32_gemm_bias_relu(gpu):
     """Config 1's module shape (smaller): every tensor on the device; equal to
-    the host-buffer run; no copy time; graph replay on the second call."""
+    the host-buffer run; no copy time; a direct launch (one kernel)."""
     torch = gpu
     M, K, N = 512, 384, 256
     r = np.random.default_rng(0)
@@ -80,12 +80,14 @@ def test_device_tensors_f32_gemm_bias_relu(gpu):
         assert np.array_equal(Y.cpu().numpy(), host_out)
         assert s.cuda_copy_in_ms < 0.5 and s.cuda_copy_out_ms < 0.5
     mdl.close()
-    assert paths[0].startswith("hip_native_graph_capture") and paths[1].startswith("hip_native_graph_replay"), paths
+    # one kernel and no copies: launched directly, no graph of one node
+    assert all(p.startswith("hip_native:") for p in paths), paths
 
 
 def test_device_tensors_rebind_and_mixed(gpu):
-    """New device addresses re-capture the graph (the old one baked in the old
-    ones); host and device tensors in one call; a host run after device runs."""
+    """New device addresses capture a new graph (a graph bakes in the addresses
+    it was captured with); host and device tensors in one call; a host run
+    after device runs."""
     torch = gpu
     M, K, N = 256, 128, 192
     r = np.random.default_rng(1)
@@ -98,6 +100,7 @@ def test_device_tensors_rebind_and_mixed(gpu):
         assert st == 0
         cases.append((x, w, b, ref.copy()))
     outs = [torch.empty((M, N), device="cuda") for _ in range(2)]
+    seen = set()
     for i, (x, w, b, ref) in enumerate(cases):
         X, W = torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda()
         Y = outs[i % 2]
@@ -105,7 +108,11 @@ def test_device_tensors_rebind_and_mixed(gpu):
         # x on the device, w on the device, bias from host memory, output on the device
         rc, s = _run(mdl, [_dt(X, abi.DTYPE_F32), _dt(W, abi.DTYPE_F32), _ht(b, abi.DTYPE_F32)], [_dt(Y, abi.DTYPE_F32)])
         assert rc == 0, s.execution_path
-        assert "graph_capture" in s.execution_path.decode()  # new input addresses every time
+        # a graph bakes in device addresses: new ones are captured, addresses
+        # the allocator handed out again replay the graph kept for them
+        key = (X.data_ptr(), W.data_ptr(), Y.data_ptr())
+        assert ("graph_replay" if key in seen else "graph_capture") in s.execution_path.decode(), (key, seen)
+        seen.add(key)
         assert np.array_equal(Y.cpu().numpy(), ref), f"case {i}"
         # host output from the same device inputs
         host_y = np.zeros((M, N), np.float32)
