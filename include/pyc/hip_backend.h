@@ -42,11 +42,12 @@ int pyc_hip_gemm_dispatch(
 /* Measured autotune of the [M,K]x[K,N] GEMM at a live shape (the reference's
  * compiler_api.c:3000-3044 records one estimated candidate per run instead):
  * every registered variant of `dtype` (PYC_DTYPE_F32/BF16/F16) whose right
- * operand is [K,N] is launched `iters` times on scratch operands and timed
- * by HIP events; the fastest becomes the symbol the backend plans for GEMMs
- * of that dtype and shape. Writes up to `cap` symbols (each in a slot of
- * `sym_stride` bytes of `syms`) and their mean ms. Returns the number timed,
- * 0 without a GPU, -1 on bad arguments. */
+ * operand is [K,N] is timed by HIP events on scratch operands of uniform
+ * [-1,1) values, after 50 ms of settling load, in three interleaved rounds of
+ * `iters` launches; the fastest median becomes the symbol the backend plans
+ * for GEMMs of that dtype and shape. Writes up to `cap` symbols (each in a
+ * slot of `sym_stride` bytes of `syms`) and their median per-launch ms.
+ * Returns the number timed, 0 without a GPU, -1 on bad arguments. */
 int pyc_hip_autotune_gemm(
     pyc_dtype dtype, int M, int N, int K, int iters,
     char* syms, size_t sym_stride, double* ms, int cap);
