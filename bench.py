@@ -78,7 +78,13 @@ _LAST_SETTLE: dict = {}
 def time_launches(torch, launch, steps: int, warmup: int, settle_ms: float = 0.0):
     """Settle the clock, warm up, then time `steps` launches: total bracketed
     by synchronize, and each launch between HIP events recorded on the stream
-    it runs on."""
+    it runs on. Returns (wall ms per step, device ms per launch, per-launch
+    ms). The device ms per launch is the span from the first launch's start
+    event to the last one's end event over `steps`: back to back, the command
+    processor readies each dispatch while the previous kernel runs, so for a
+    kernel of tens of microseconds this is its own duration, where one
+    event pair around a single launch also holds the dispatch latency (the
+    per-launch list, reported as latency_ms)."""
     stream = torch.cuda.current_stream()
     _LAST_SETTLE.clear()
     if settle_ms > 0:
@@ -96,9 +102,10 @@ def time_launches(torch, launch, steps: int, warmup: int, settle_ms: float = 0.0
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
     per = [e0.elapsed_time(e1) for e0, e1 in evs]
+    span = evs[0][0].elapsed_time(evs[-1][1]) / steps
     _LAST_LATENCY.clear()
     _LAST_LATENCY.update(latency_stats(per))
-    return wall_ms / steps, float(np.mean(per)), per
+    return wall_ms / steps, span, per
 
 
 # per-launch device-time statistics of the last timed loop (reported as
@@ -537,6 +544,68 @@ def wl_engine_cfg1(torch, args):
     return res
 
 
+def wl_engine_bf16(torch, args):
+    """BASELINE config 2's GEMM as a module through pyc_run_model: in,in,
+    matmul,out in bf16 with the weight stored [K,N] (the IR's matmul layout,
+    the reference's default cutlass_gemm_tensorcore_bf16 symbol), every tensor
+    resident in device memory, one pyc_run_model call per step timed by wall
+    clock. The plan runs the persistent LDS-DMA kernel with B staged as
+    k-rows."""
+    from pyc_amd import abi, engine
+    os.environ["PYC_HIP_STRICT"] = "1"
+    M = N = K = 8192
+    g1 = torch.Generator(device="cuda").manual_seed(1)
+    g2 = torch.Generator(device="cuda").manual_seed(2)
+    X = (torch.randn((M, K), generator=g1, device="cuda") / np.sqrt(K)).to(torch.bfloat16)
+    W = torch.randn((K, N), generator=g2, device="cuda").to(torch.bfloat16)
+    Y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    BF = abi.DTYPE_BF16
+    ops = [engine.op(abi.OP_INPUT, "x", (M, K), dtype=BF), engine.op(abi.OP_INPUT, "w", (K, N), dtype=BF),
+           engine.op(abi.OP_MATMUL, "matmul0", (), (0, 1), dtype=BF),
+           engine.op(abi.OP_OUTPUT, "out0", (M, N), (2,), dtype=BF)]
+    model = engine.Model(ops, backend=abi.BACKEND_CUDA)
+    if model.status != 0:
+        raise RuntimeError(f"pyc_compile_model failed: {model.status}")
+    run = model.bind([engine.device_tensor(X, BF), engine.device_tensor(W, BF)], [engine.device_tensor(Y, BF)])
+    torch.cuda.synchronize()
+
+    def call():
+        rc, st = run()
+        if rc != 0:
+            raise RuntimeError(f"pyc_run_model failed ({rc}): {st.execution_path.decode()}")
+        return st
+
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < args.settle_ms:
+        call()
+    for _ in range(args.warmup):
+        call()
+    stats, wall = [], []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        t1 = time.perf_counter()
+        stats.append(call())
+        wall.append((time.perf_counter() - t1) * 1e3)
+    ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    eng = engine.run_stats_json(stats, wall, model)
+    model.close()
+    if not eng["execution_path"].startswith("hip_native"):
+        raise RuntimeError(f"engine run did not take the native path: {eng['execution_path']}")
+    flops = 2.0 * M * N * K
+    kernel_ms = eng["profile"]["cuda_kernel_ms"]
+    return {
+        "value": flops / (ms_step * 1e-3) / 1e12, "unit": "TFLOP/s", "ms_per_step": ms_step, "dtype": "bf16",
+        "config": {"workload": "engine_pyc_run_model_gemm_bf16_kn_8192", "M": M, "N": N, "K": K,
+                   "tensors": "device-resident", "weight_layout": "[K,N]", "module": "input,input,matmul,output"},
+        "roofline": {"bound": "mfma", "achieved": flops / (kernel_ms * 1e-3) / 1e12, "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": flops / (kernel_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+                     "traffic": load_traffic("gemm_bf16_nn_8192"), "kernel_ms": kernel_ms},
+        "latency_ms": eng.pop("latency_ms"),
+        "engine": eng,
+        "vs_baseline": None,
+    }
+
+
 def _eltwise_line(name, config, nbytes, ms_step, ms_kernel):
     return {
         "value": nbytes / (ms_step * 1e-3) / 1e9, "unit": "GB/s", "ms_per_step": ms_step, "dtype": "bf16",
@@ -579,6 +648,7 @@ def wl_layernorm(torch, args):
 
 WORKLOADS = {"gemm_bf16": wl_gemm_bf16, "gemm_bf16_nn": wl_gemm_bf16_nn, "gemm_f32_cfg1": wl_gemm_f32_cfg1, "decode_chain": wl_decode_chain,
              "attention": wl_attention, "conv": wl_conv, "engine_cfg1": wl_engine_cfg1,
+             "engine_bf16": wl_engine_bf16,
              "gelu": wl_gelu, "layernorm": wl_layernorm}
 
 
