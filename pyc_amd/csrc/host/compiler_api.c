@@ -978,20 +978,29 @@ static int autotune_persist(const char* path, const char* op, pyc_backend backen
 }
 
 /* On the GPU backend the first run with enable_autotune measures every
- * registered tile variant of the module's first [M,K]x[K,N] GEMM at its live
- * shape (pyc_hip_autotune_gemm, HIP-event timings). Each result updates the
- * registry's "matmul" entry of that symbol and is persisted as an
- * `matmul_fused|backend|symbol|best_ms` line; the fastest is promoted and
- * becomes the plan's symbol for that shape. Without a GPU nothing is timed
- * and the per-run estimate below stays in force. */
+ * registered tile variant of each distinct [M,K]x[K,N] GEMM shape of the
+ * module at its live shape (pyc_hip_autotune_gemm, HIP-event timings), which
+ * makes the fastest the planned symbol for that shape. Each result updates
+ * the registry's "matmul" entry of that symbol and is persisted as a
+ * `matmul_fused|backend|symbol|best_ms` line; the winner at the module's
+ * largest GEMM (by M*N*K) is promoted in the registry. Without a GPU nothing
+ * is timed and the per-run estimate below stays in force. */
 static void measured_autotune(pyc_compiled_model* model, const pyc_ir_module* m) {
+    enum { MAX_SHAPES = 16 };
     char syms[16][PYC_KERNEL_SYMBOL_MAX];
+    char promote[PYC_KERNEL_SYMBOL_MAX] = "";
     double ms[16];
+    double promote_work = -1.0;
+    int64_t seen[MAX_SHAPES][4];
+    size_t nseen = 0;
     size_t i;
-    int n, j, best = 0;
+    int n, j, best;
     for (i = 0; i < m->op_count; ++i) {
         const pyc_ir_op* op = &m->ops[i];
         const pyc_ir_op *a, *b;
+        int64_t key[4];
+        size_t k;
+        int dup = 0;
         if (op->kind != PYC_IR_OP_MATMUL || op->input_count < 2 || op->input_ids[0] < 0 || op->input_ids[1] < 0 ||
             (size_t)op->input_ids[0] >= m->op_count || (size_t)op->input_ids[1] >= m->op_count) {
             continue;
@@ -999,13 +1008,25 @@ static void measured_autotune(pyc_compiled_model* model, const pyc_ir_module* m)
         a = &m->ops[op->input_ids[0]];
         b = &m->ops[op->input_ids[1]];
         if (a->shape.rank != 2 || b->shape.rank != 2 || a->shape.dims[1] != b->shape.dims[0] || a->dtype != b->dtype) {
-            return;
+            continue; /* not an [M,K]x[K,N] GEMM of one dtype (an fp8 weight, say) */
         }
-        n = pyc_hip_autotune_gemm(a->dtype, (int)a->shape.dims[0], (int)b->shape.dims[1], (int)a->shape.dims[1], 10,
-                                  &syms[0][0], PYC_KERNEL_SYMBOL_MAX, ms, 16);
+        key[0] = (int64_t)a->dtype;
+        key[1] = a->shape.dims[0];
+        key[2] = b->shape.dims[1];
+        key[3] = a->shape.dims[1];
+        for (k = 0; k < nseen; ++k) {
+            dup |= memcmp(seen[k], key, sizeof(key)) == 0;
+        }
+        if (dup || nseen == MAX_SHAPES) {
+            continue;
+        }
+        memcpy(seen[nseen++], key, sizeof(key));
+        n = pyc_hip_autotune_gemm(a->dtype, (int)key[1], (int)key[2], (int)key[3], 10, &syms[0][0],
+                                  PYC_KERNEL_SYMBOL_MAX, ms, 16);
         if (n <= 0) {
-            return;
+            continue;
         }
+        best = 0;
         for (j = 0; j < n; ++j) {
             (void)pyc_kernel_benchmark_update_symbol("matmul", model->backend, syms[j], ms[j]);
             if (autotune_persist(model->autotune_db, "matmul_fused", model->backend, syms[j], ms[j]) == 0) {
@@ -1015,9 +1036,14 @@ static void measured_autotune(pyc_compiled_model* model, const pyc_ir_module* m)
                 best = j;
             }
         }
-        (void)pyc_kernel_promote_symbol("matmul", model->backend, syms[best]);
+        if ((double)key[1] * (double)key[2] * (double)key[3] > promote_work) {
+            promote_work = (double)key[1] * (double)key[2] * (double)key[3];
+            copy_str(promote, sizeof(promote), syms[best]);
+        }
         model->hip_tuned = 1;
-        return;
+    }
+    if (promote[0]) {
+        (void)pyc_kernel_promote_symbol("matmul", model->backend, promote);
     }
 }
 

@@ -88,3 +88,35 @@ def test_run_model_autotune(gpu, dt, tmp_path, monkeypatch):
     for tune, y in outs.items():
         got = oracle.bf16_to_f32(y) if dt == abi.DTYPE_BF16 else y
         assert rel_max_err(got, ref) <= (2e-2 if dt == abi.DTYPE_BF16 else 1e-5), tune
+
+
+def test_run_model_autotune_every_gemm_shape(gpu, tmp_path, monkeypatch):
+    """A module with two GEMMs of different shapes (x W1 -> ReLU -> W2, bf16):
+    autotune times both shapes on the first run (each shape's variants are
+    persisted and the shape is planned with its fastest), and the tuned
+    module still matches the oracle."""
+    monkeypatch.setenv("PYC_HIP_STRICT", "1")
+    M, D, F = 512, 256, 768
+    r = np.random.default_rng(12)
+    x = oracle.f32_to_bf16(r.uniform(-1, 1, (M, D)).astype(np.float32))
+    w1 = oracle.f32_to_bf16((r.uniform(-1, 1, (D, F)) / 16).astype(np.float32))
+    w2 = oracle.f32_to_bf16((r.uniform(-1, 1, (F, D)) / 16).astype(np.float32))
+    BF = abi.DTYPE_BF16
+    ops = [engine.op(abi.OP_INPUT, "x", (M, D), dtype=BF), engine.op(abi.OP_INPUT, "w1", (D, F), dtype=BF),
+           engine.op(abi.OP_INPUT, "w2", (F, D), dtype=BF), engine.op(abi.OP_MATMUL, "mm1", (), (0, 1), dtype=BF),
+           engine.op(abi.OP_RELU, "relu1", (), (3,), dtype=BF), engine.op(abi.OP_MATMUL, "mm2", (), (4, 2), dtype=BF),
+           engine.op(abi.OP_OUTPUT, "o", (M, D), (5,), dtype=BF)]
+    db = tmp_path / "tune.db"
+    mdl = engine.Model(ops, backend=abi.BACKEND_CUDA, enable_autotune=1, autotune_db_path=str(db).encode())
+    assert mdl.status == 0
+    y = np.zeros((M, D), np.uint16)
+    for _ in range(2):
+        rc, st = mdl.run([engine.host_tensor(a, BF) for a in (x, w1, w2)], [engine.host_tensor(y, BF)])
+        assert rc == 0 and st.execution_path.decode().startswith("hip_native"), st.execution_path
+    mdl.close()
+    assert st.autotune_saved == 1
+    lines = [ln.split("|") for ln in db.read_text().splitlines() if ln.strip()]
+    assert len(lines) >= 2 and all(float(ln[3]) > 0 for ln in lines)
+    h = oracle.bf16_to_f32(oracle.f32_to_bf16(np.maximum(oracle.gemm_bf16(x, w1, False), 0)))
+    ref = oracle.gemm_bf16(oracle.f32_to_bf16(h), w2, False)
+    assert rel_max_err(oracle.bf16_to_f32(y), ref) <= 2e-2
