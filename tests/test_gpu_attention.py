@@ -102,6 +102,34 @@ def test_attention_config3_sampled_heads(gpu):
     torch.testing.assert_close(O[:, :, 0].float(), V[:, :, 0].float(), rtol=2 ** -7, atol=1e-3)
 
 
+def test_attention_config3_every_head_vs_torch_fp32(gpu):
+    """Config 3 at full size, all 256 (b,h) heads against a plain PyTorch fp32
+    reference of the same op (scores, causal mask, softmax and P.V in fp32 on the
+    device, one batch at a time), with the same bounds as the oracle checks."""
+    torch = gpu
+    B, H, S, D = 8, 32, 2048, 128
+    gens = [torch.Generator(device="cuda").manual_seed(s) for s in (3, 4, 5)]
+    Q, K, V = (torch.randn((B, H, S, D), generator=g, device="cuda").to(torch.bfloat16) for g in gens)
+    O = torch.empty_like(Q)
+    scale = 1.0 / np.sqrt(D)
+    pyc_amd.attention("hip_attention_bf16", Q, K, V, O, True, scale)
+    torch.cuda.synchronize()
+    mask = torch.ones((S, S), dtype=torch.bool, device="cuda").triu(1)
+    worst = 0.0
+    for b in range(B):
+        q, k, v = (t[b].float() for t in (Q, K, V))
+        sc = torch.matmul(q, k.transpose(-1, -2).contiguous()) * scale
+        sc.masked_fill_(mask, float("-inf"))
+        ref = torch.matmul(torch.softmax(sc, dim=-1), v)
+        del sc
+        got = O[b].float()
+        err = (got - ref).abs()
+        worst = max(worst, float(err.max() / ref.abs().max()))
+        bound = 2.0 ** -7 * ref.abs() + 1e-2 * ref.abs().max()
+        assert not bool((err > bound).any()), f"batch {b}: {int((err > bound).sum())} off"
+    assert worst <= 2e-2, worst
+
+
 def test_attention_f16_and_reference_abi(gpu):
     torch = gpu
     S, D = 192, 128
