@@ -140,6 +140,21 @@ def _host_cores() -> int:
         return os.cpu_count() or 1
 
 
+def _host_info() -> dict:
+    """The CPU the cpu_baseline legs ran on: model name, logical CPUs of the
+    machine and the ones this process may use."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "nproc": os.cpu_count(), "cores_available": _host_cores()}
+
+
 def cpu_baseline_gemm(a_rows_f32: np.ndarray, b_kn_f32: np.ndarray, full_flops: float, sample_desc: str,
                       threads: int | None = None):
     """Time the reference CPU executor on a[rows] @ b (fp32) and scale to the
@@ -713,6 +728,7 @@ def main() -> int:
     line.update(nested)
     line["device"] = {"arch": info.gcn_arch.decode(), "cus": info.compute_units,
                       "sclk_mhz": info.clock_khz / 1e3}
+    line["host"] = _host_info()
     print(json.dumps(line), flush=True)
     return 0
 
