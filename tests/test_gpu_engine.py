@@ -93,6 +93,65 @@ def test_graph_cache_two_models_alternating():
     assert all("graph_replay" in p for p in pa[2:] + pb[2:]), (pa, pb)
 
 
+def test_graph_cache_eviction_many_models():
+    """Ten models of different shapes run round-robin three times: more run
+    signatures than the backend keeps graphs for, so graphs are evicted and
+    re-captured on the way; every call matches the oracle."""
+    r = np.random.default_rng(8)
+    cases = []
+    for i in range(10):
+        M, K, N = 64 + 32 * i, 96, 128 + 64 * (i % 3)
+        x = r.uniform(-1, 1, (M, K)).astype(np.float32)
+        w = r.uniform(-1, 1, (K, N)).astype(np.float32)
+        b = r.uniform(-1, 1, N).astype(np.float32)
+        ops = [eu.op(abi.OP_INPUT, "x", (M, K)), eu.op(abi.OP_INPUT, "w", (K, N)), eu.op(abi.OP_INPUT, "bias", (N,)),
+               eu.op(abi.OP_MATMUL, "matmul0", (), (0, 1)), eu.op(abi.OP_ADD, "add0", (), (3, 2)),
+               eu.op(abi.OP_RELU, "relu0", (), (4,)), eu.op(abi.OP_OUTPUT, "out0", (M, N), (5,))]
+        mdl = eu.Model(eu.mine(), ops, backend=abi.BACKEND_CUDA)
+        assert mdl.status == 0
+        cases.append((mdl, (x, w, b), (M, N), oracle.gemm_bias_relu_f32(x, w, b, relu=True)))
+    for _ in range(3):
+        for mdl, ins, shape, ref in cases:
+            st, (out,), s = mdl.run(list(ins), [shape])
+            assert st == 0
+            _native(s)
+            assert rel_max_err(out, ref) <= 1e-4
+    for mdl, _, _, _ in cases:
+        mdl.close()
+
+
+def test_static_rhs_weight_reuploaded_after_other_model(monkeypatch):
+    """PYC_CUDA_ASSUME_STATIC_RHS skips re-uploading a weight whose host buffer
+    did not change. The device buffers are per op id, and another model's
+    value with the same op id (here a GELU output, op 1, the weight's id in
+    the GEMM model) overwrites the uploaded weight: the next run of the GEMM
+    model must upload it again."""
+    monkeypatch.setenv("PYC_CUDA_ASSUME_STATIC_RHS", "1")
+    r = np.random.default_rng(9)
+    M, K, N = 128, 64, 96
+    x = r.uniform(-1, 1, (M, K)).astype(np.float32)
+    w = r.uniform(-1, 1, (K, N)).astype(np.float32)
+    b = r.uniform(-1, 1, N).astype(np.float32)
+    ops = [eu.op(abi.OP_INPUT, "x", (M, K)), eu.op(abi.OP_INPUT, "w", (K, N)), eu.op(abi.OP_INPUT, "bias", (N,)),
+           eu.op(abi.OP_MATMUL, "matmul0", (), (0, 1)), eu.op(abi.OP_ADD, "add0", (), (3, 2)),
+           eu.op(abi.OP_RELU, "relu0", (), (4,)), eu.op(abi.OP_OUTPUT, "out0", (M, N), (5,))]
+    gemm = eu.Model(eu.mine(), ops, backend=abi.BACKEND_CUDA)
+    z = r.uniform(-3, 3, (K, N)).astype(np.float32)
+    gops = [eu.op(abi.OP_INPUT, "z", (K, N)), eu.op(abi.OP_GELU, "gelu0", (), (0,)),
+            eu.op(abi.OP_OUTPUT, "out0", (K, N), (1,))]
+    gelu = eu.Model(eu.mine(), gops, backend=abi.BACKEND_CUDA)
+    assert gemm.status == 0 and gelu.status == 0
+    ref = oracle.gemm_bias_relu_f32(x, w, b, relu=True)
+    for _ in range(3):
+        st, (out,), s = gemm.run([x, w, b], [(M, N)])
+        assert st == 0 and _native(s)
+        assert rel_max_err(out, ref) <= 1e-4
+        st, (g,), s = gelu.run([z], [(K, N)])
+        assert st == 0 and _native(s)
+    gemm.close()
+    gelu.close()
+
+
 def test_bf16_matmul_module_nn():
     m, k, n = 320, 256, 192
     r = np.random.default_rng(1)
