@@ -623,8 +623,8 @@ __global__ void __launch_bounds__(kCWaves * kWave, 1) w8a16_chain_kernel(W8Chain
         u32x4 w;
         u32x4 x[2][2];
     };
-    auto read_frag = [&](int n, QFrag& f) {
-        const uint8_t* stage = smem + (n % ST) * kQStageBytes;
+    auto read_frag = [&](int stg, QFrag& f) {
+        const uint8_t* stage = smem + stg * kQStageBytes;
         f.w = *reinterpret_cast<const u32x4*>(stage + w_rd);
 #pragma unroll
         for (int h = 0; h < 2; ++h)
@@ -753,7 +753,13 @@ __global__ void __launch_bounds__(kCWaves * kWave, 1) w8a16_chain_kernel(W8Chain
                 }
             };
 
-            int seg_start = i0;
+            // segment bookkeeping by running positions (no divisions per item):
+            // item n is k-item c_kk of unit c_unit; seg_whole says the current
+            // segment began at the unit's first k-item
+            int c_unit = u0, c_kk = kk0;
+            bool seg_whole = kk0 == 0;
+            int d_stg = ST - 1;  // ring stage of the next load (item n + ST - 1 at iteration n)
+            int c_stg = 0;       // ring stage of item n
             int pend_unit = -1, last_unit = -1;
             f32x4 accs[2][2];
 #pragma unroll
@@ -769,9 +775,9 @@ __global__ void __launch_bounds__(kCWaves * kWave, 1) w8a16_chain_kernel(W8Chain
                 wait_first_items<ST>(n);
                 __syncthreads();  // every wave's loads; item n-1's stage is free
                 {
-                    const int stg = (n + ST - 1) % ST;
-                    dma_w(wrs, K, d_unit, d_kk, stg);
-                    dma_x(xrs, xvo, d_kk, stg);
+                    dma_w(wrs, K, d_unit, d_kk, d_stg);
+                    dma_x(xrs, xvo, d_kk, d_stg);
+                    d_stg = d_stg + 1 == ST ? 0 : d_stg + 1;
                     if (d_left > 1) {  // advance; past the last item keep reloading it
                         --d_left;
                         if (++d_kk == kitems) {
@@ -780,7 +786,8 @@ __global__ void __launch_bounds__(kCWaves * kWave, 1) w8a16_chain_kernel(W8Chain
                         }
                     }
                 }
-                if (n + 1 < nitems) read_frag(n + 1, nxt);
+                c_stg = c_stg + 1 == ST ? 0 : c_stg + 1;
+                if (n + 1 < nitems) read_frag(c_stg, nxt);
                 {
                     const u32x4 w0 = fp8x8_to_bf16x8(cur.w[0], cur.w[1]);
                     const u32x4 w1 = fp8x8_to_bf16x8(cur.w[2], cur.w[3]);
@@ -790,9 +797,17 @@ __global__ void __launch_bounds__(kCWaves * kWave, 1) w8a16_chain_kernel(W8Chain
                         acc[h] = mfma16x16x32(w1, cur.x[h][1], acc[h], bf16_t{});
                     }
                 }
-                const int item = i0 + n;
-                if (n != nitems - 1 && (item + 1) % kitems != 0) return;  // segment goes on
-                const int unit = item / kitems;
+                const bool unit_end = c_kk == kitems - 1;
+                const int unit = c_unit;
+                const bool whole = seg_whole && unit_end;  // no other workgroup contributes
+                if (unit_end) {
+                    c_kk = 0;
+                    ++c_unit;
+                } else {
+                    ++c_kk;
+                }
+                if (n != nitems - 1 && !unit_end) return;  // segment goes on
+                seg_whole = true;  // a segment that ends at a unit's end is followed by one that starts a unit
                 f32x4 v[2] = {accs[0][0] + accs[1][0], accs[0][1] + accs[1][1]};
                 // the two k halves of a channel block meet in waves 0..3
                 if (jh == 1) {
@@ -808,14 +823,13 @@ __global__ void __launch_bounds__(kCWaves * kWave, 1) w8a16_chain_kernel(W8Chain
                 for (int a2 = 0; a2 < 2; ++a2) accs[a2][0] = accs[a2][1] = f32x4{0.f, 0.f, 0.f, 0.f};
                 if (jh == 1) {
                     // waves 4..7 only track the segment state
-                    if (!(seg_start == unit * kitems && item == unit * kitems + kitems - 1)) {
+                    if (!whole) {
                         if (n != nitems - 1) pend_unit = unit;
                         else last_unit = unit;
                     }
-                    seg_start = item + 1;
                     return;
                 }
-                if (seg_start == unit * kitems && item == unit * kitems + kitems - 1) {
+                if (whole) {
                     q_store_y(unit, v);  // whole unit: no other contributor
                 } else if (n != nitems - 1) {
                     pend_unit = unit;  // arrival counted after the last item
@@ -824,9 +838,6 @@ __global__ void __launch_bounds__(kCWaves * kWave, 1) w8a16_chain_kernel(W8Chain
                     last_unit = unit;
                     q_publish(unit, v);
                 }
-                seg_start = item + 1;
-#pragma unroll
-                for (int a2 = 0; a2 < 2; ++a2) accs[a2][0] = accs[a2][1] = f32x4{0.f, 0.f, 0.f, 0.f};
             };
 
             wait_first_items<ST>(0);  // items 0 and 1 landed (see process) ...
