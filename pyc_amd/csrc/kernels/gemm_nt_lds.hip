@@ -285,7 +285,7 @@ gemm_nt_lds4k64_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
 // a row gathers one whole line, and taps that fall into the padding get an
 // offset past the end of x, which the buffer descriptor reads as zeros.
 struct ConvGeomP {
-    int H, W, C, P, Q, S, sh, sw, ph, pw;
+    int H, W, C, P, Q, R, S, sh, sw, ph, pw;
     uint32_t x_bytes;
 };
 
@@ -377,16 +377,22 @@ gemm_nt_persist_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
     // swizzled chunk is the same for every row it loads (rows it loads differ
     // by multiples of 8, and the swizzle sees row & 7).
     struct StageTap {
-        int r, s, c0;
+        int r, s, c0, koff;
     };
+    // Channel-major stage order: the 64-channel chunks outside, the R*S taps
+    // inside, so the x lines of one chunk are re-read by all taps while they
+    // are still in L2 (tap-major order re-fetched x from HBM about 3.5x).
+    // koff is the stage's first GEMM k, (r*S + s)*C + c0, the filter's column.
     auto stage_tap = [&](int kt) {
-        StageTap t{0, 0, 0};
+        StageTap t{0, 0, 0, kt * BK};
         if constexpr (CONV) {
-            const int cst = cg.C / BK;
-            const int tap = kt / cst;
-            t.c0 = (kt - tap * cst) * BK;
+            const int ntap = cg.R * cg.S;
+            const int chunk = kt / ntap;
+            const int tap = kt - chunk * ntap;
+            t.c0 = chunk * BK;
             t.r = tap / cg.S;
             t.s = tap - t.r * cg.S;
+            t.koff = tap * cg.C + t.c0;
         }
         return t;
     };
@@ -402,7 +408,8 @@ gemm_nt_persist_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
             lds_dma_buf_b128_u(a_rsrc, off, 0u, ldso[j] + (uint32_t)buf * STAGE_BYTES);
         } else {
             // stage kt of B starts at k-row 64 kt ([K,N]) or at column 64 kt ([N,K])
-            const uint32_t soff = (BNN && j >= LOADS) ? (uint32_t)kt * (uint32_t)(BK * N * 2) : (uint32_t)(kt * BK * 2);
+            const uint32_t soff = (BNN && j >= LOADS) ? (uint32_t)kt * (uint32_t)(BK * N * 2)
+                                  : CONV ? (uint32_t)(tp.koff * 2) : (uint32_t)(kt * BK * 2);
             lds_dma_buf_b128(j < LOADS ? a_rsrc : b_rsrc, voff[j], soff, ldso[j] + (uint32_t)buf * STAGE_BYTES);
         }
     };
@@ -720,7 +727,7 @@ extern "C" int pyc_hip_conv2d_persist_launch(int is_bf16, int Nimg, int H, int W
     }
     const int tiles_m = (int)(M / kD_BM), tiles_n = Kout / kD_BN;
     const int ntiles = tiles_m * tiles_n;
-    const ConvGeomP cg{H, W, C, P, Q, S, sh, sw, ph, pw, (uint32_t)xb};
+    const ConvGeomP cg{H, W, C, P, Q, R, S, sh, sw, ph, pw, (uint32_t)xb};
     const int epi = ((bias != nullptr) ? 1 : 0) | (relu ? 2 : 0);
     const dim3 grid(ntiles < n_cu ? ntiles : n_cu), block(4 * kWave);
     hipStream_t st = (hipStream_t)stream;
