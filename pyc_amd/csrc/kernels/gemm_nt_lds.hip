@@ -309,7 +309,7 @@ gemm_nt_persist_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: per-wave offsets stay scalar
     const int wm = wave >> 1;
     const int wn = wave & 1;
     const int lrow = lane & 15;
@@ -339,10 +339,15 @@ gemm_nt_persist_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
     // input coordinates of tap (0,0), ((ih + 32768) << 16) | (iw + 32768) (hw[j]).
     uint32_t hw[CONV ? LOADS : 1];
     auto set_tile = [&](int m0, int n0) {
+        // lane index made opaque, so that the per-row constants below are
+        // recomputed here (a few ALU operations) instead of being hoisted out
+        // of the tile loop and spilled
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
 #pragma unroll
         for (int j = 0; j < LOADS; ++j) {
-            const int row = (j * 4 + wave) * ROWS_PER_LOAD + lane / CH;
-            const int lch = d_swz(row, lane % CH);
+            const int row = (j * 4 + wave) * ROWS_PER_LOAD + ln / CH;
+            const int lch = d_swz(row, ln % CH);
             if constexpr (CONV) {
                 const int m = m0 + row;
                 const int n = m / (cg.P * cg.Q);
@@ -358,12 +363,24 @@ gemm_nt_persist_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
                 // DMA load j of B moves k-rows 2q, 2q+1 (q = 4j + wave) of the
                 // [64 k][256 n] stage; lane i: k-row 2q + i/32, physical chunk
                 // i%32 holding logical chunk (i%32) ^ nn_swz(k-row)
-                const int brow = 2 * (j * 4 + wave) + lane / 32;
-                const int bch = (lane % 32) ^ nn_swz(brow);
+                const int brow = 2 * (j * 4 + wave) + ln / 32;
+                const int bch = (ln % 32) ^ nn_swz(brow);
                 voff[LOADS + j] = (uint32_t)(((size_t)brow * N + n0 + bch * 8) * 2);
             } else {
                 voff[LOADS + j] = (uint32_t)(((size_t)(n0 + row) * K + lch * 8) * 2);
             }
+        }
+        // Every offset is complete here, before the tile's first DMA is issued.
+        // Without this the compiler interleaves the offset arithmetic with the
+        // DMAs, and its own waits for operands reloaded from scratch in between
+        // (s_waitcnt vmcnt, which also counts the DMAs it does not see) waited
+        // for the DMAs issued so far: the next tile's loads went out one memory
+        // round trip apart.
+#pragma unroll
+        for (int j = 0; j < 2 * LOADS; ++j) asm volatile("" : "+v"(voff[j]));
+        if constexpr (CONV) {
+#pragma unroll
+            for (int j = 0; j < LOADS; ++j) asm volatile("" : "+v"(hw[j]));
         }
     };
 #pragma unroll
@@ -437,11 +454,9 @@ gemm_nt_persist_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
     const int g16 = lane >> 4;
     const int bsw = nn_swz(8 * g16 + (lrow >> 2));
     const uint16_t* const b_nn = Bs + (8 * g16 + (lrow >> 2)) * 256 + wn * 128 + ((lrow & 3) >> 1) * 8 + (lrow & 1) * 4;
+    // per-fragment chunk offsets of the [K,N] reads, set at the top of every
+    // tile (see there)
     int b_jo[BNN ? 8 : 1];
-    if constexpr (BNN) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) b_jo[j] = ((2 * j) ^ bsw) * 8;
-    }
     auto read_b = [&](int h, int j, uint32_t bufo) {
         if constexpr (BNN) {
             const uint16_t* p = b_nn + bufo + b_jo[j] + h * 32 * 256;
@@ -467,6 +482,15 @@ gemm_nt_persist_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
     bool stores_pending = false;  // the previous tile's NSTORE stores follow this tile's prologue loads
 
     for (;;) {
+        if constexpr (BNN) {
+            // recomputed per tile from an opaque copy of the swizzle: computed
+            // once, they stayed live through the epilogue, were spilled there
+            // and came back as eight serialized scratch reloads at the tile top
+            int sw = bsw;
+            asm volatile("" : "+v"(sw));
+#pragma unroll
+            for (int j = 0; j < 8; ++j) b_jo[j] = ((2 * j) ^ sw) * 8;
+        }
         // stage 0 landed (stage 1 and the previous tile's stores may be in flight)
         if (stores_pending) wait_vmem_le<2 * LOADS + NSTORE>();
         else wait_vmem_le<2 * LOADS>();

@@ -116,7 +116,10 @@ __device__ inline void w8_mma(f32x4 (&acc)[4][2], const W8Item& f) {
 // split-K partials. The caller waits (s_waitcnt vmcnt) before relying on them:
 // these are asm, so the compiler does not track them.
 __device__ inline void store_coherent_b128(float* p, const f32x4& v) {
-    asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+    // s_nop: the one wait state a store of more than 8 bytes needs before a
+    // VALU instruction may overwrite its data registers (the compiler does not
+    // insert it after inline asm)
+    asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 0" : : "v"(p), "v"(v) : "memory");
 }
 __device__ inline f32x4 load_coherent_b128(const float* p) {
     f32x4 v;

@@ -291,6 +291,37 @@ def test_conv_and_attention_modules():
     assert rel_max_err(oracle.bf16_to_f32(out), ref) <= 2e-2
 
 
+def test_conv_module_persistent_graph_replay():
+    """A conv module on the persistent kernel (98 tiles of 256 x 256) through
+    pyc_run_model: three runs (capture, two replays) give identical outputs,
+    which match the oracle on the first and last image."""
+    r = np.random.default_rng(9)
+    N, H, W, C, K = 8, 56, 56, 256, 256
+    x = oracle.f32_to_bf16(r.uniform(0, 1, (N, H, W, C)).astype(np.float32))
+    w = oracle.f32_to_bf16(r.normal(0, np.sqrt(2.0 / (9 * C)), (K, 3, 3, C)).astype(np.float32))
+    ops = [eu.op(abi.OP_INPUT, "x", (N, H, W, C), dtype=abi.DTYPE_BF16),
+           eu.op(abi.OP_INPUT, "w", (K, 3, 3, C), dtype=abi.DTYPE_BF16),
+           eu.op(abi.OP_CONV2D, "conv@s1x1p1x1", (), (0, 1), dtype=abi.DTYPE_BF16),
+           eu.op(abi.OP_OUTPUT, "y", (N, H, W, K), (2,), dtype=abi.DTYPE_BF16)]
+    mdl = eu.Model(eu.mine(), ops, backend=abi.BACKEND_CUDA)
+    outs, paths = [], []
+    for _ in range(3):
+        st, (out,), s = mdl.run([x, w], [(N, H, W, K)], in_dtypes=[abi.DTYPE_BF16, abi.DTYPE_BF16],
+                                out_dtypes=[abi.DTYPE_BF16], out_np_dtype=np.uint16)
+        assert st == 0
+        paths.append(_native(s))
+        outs.append(out)
+    mdl.close()
+    assert "graph_capture" in paths[0] and "graph_replay" in paths[-1], paths
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+    wf = oracle.bf16_to_f32(w)
+    for n in (0, N - 1):
+        ref = oracle.conv2d_nhwc_f32(oracle.bf16_to_f32(x[n:n + 1]), wf, None, (1, 1), (1, 1), False)
+        got = oracle.bf16_to_f32(outs[0].reshape(N, H, W, K)[n:n + 1])
+        assert rel_max_err(got, ref) <= 2e-2
+        assert not (np.abs(got - ref) > 2.0 ** -8 * np.abs(ref) + 4e-6 * 48 * np.abs(ref).max()).any()
+
+
 def test_no_graph_and_skip_output_copy(monkeypatch):
     monkeypatch.setenv("PYC_CUDA_ENABLE_GRAPH_REPLAY", "0")
     r = np.random.default_rng(5)
