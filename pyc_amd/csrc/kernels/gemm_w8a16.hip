@@ -699,7 +699,20 @@ __global__ void __launch_bounds__(kCWaves * kWave, 1) w8a16_chain_kernel(W8Chain
             pro_item(ST - 1, d_unit, d_kk);
             int d_left = nitems - (ST - 1);  // loads still to come before the clamp
 
-            auto q_store_y = [&](int unit, const f32x4 (&v)[2]) {
+            // scales of this lane's 4 consecutive channels of a unit
+            auto q_scale = [&](int unit, float (&sc)[4]) {
+                const int nch = unit * kW8Rows + 16 * wsub + 4 * lg;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) sc[r] = P.scale[nch + r];
+            };
+            // the same as one 16-byte asm load, for the reduction below: the
+            // caller's vmcnt wait covers it along with the partials (a load the
+            // compiler sees gets a vmcnt(0) of its own, a second round trip)
+            auto q_scale_async = [&](int unit) {
+                const int nch = unit * kW8Rows + 16 * wsub + 4 * lg;
+                return load_coherent_b128(P.scale + nch);
+            };
+            auto q_store_y = [&](int unit, const f32x4 (&v)[2], const float (&sc)[4]) {
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     const int t = 16 * h + lr;
@@ -708,7 +721,7 @@ __global__ void __launch_bounds__(kCWaves * kWave, 1) w8a16_chain_kernel(W8Chain
                     float y[4];
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        y[r] = v[h][r] * P.scale[nch + r];
+                        y[r] = v[h][r] * sc[r];
                         if (P.relu) y[r] = y[r] > 0.f ? y[r] : 0.f;
                     }
                     store_coherent_b64(P.Y + (size_t)t * N + nch,
@@ -741,7 +754,17 @@ __global__ void __launch_bounds__(kCWaves * kWave, 1) w8a16_chain_kernel(W8Chain
                         }
                     }
                 }
+                // the units' scales in the same round trip as the partials
+                f32x4 scv[2];
+#pragma unroll
+                for (int uu = 0; uu < 2; ++uu)
+                    if (ns[uu] > 0) scv[uu] = q_scale_async(uu == 0 ? u0 : u1);
                 wait_vmem_le<0>();
+                float sc[2][4];
+#pragma unroll
+                for (int uu = 0; uu < 2; ++uu)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) sc[uu][r] = scv[uu][r];
 #pragma unroll
                 for (int uu = 0; uu < 2; ++uu) {
                     if (ns[uu] == 0) continue;
@@ -752,7 +775,7 @@ __global__ void __launch_bounds__(kCWaves * kWave, 1) w8a16_chain_kernel(W8Chain
                             sum[0] += got[uu][sl][0];
                             sum[1] += got[uu][sl][1];
                         }
-                    q_store_y(uu == 0 ? u0 : u1, sum);
+                    q_store_y(uu == 0 ? u0 : u1, sum, sc[uu]);
                 }
             };
 
@@ -833,7 +856,9 @@ __global__ void __launch_bounds__(kCWaves * kWave, 1) w8a16_chain_kernel(W8Chain
                     return;
                 }
                 if (whole) {
-                    q_store_y(unit, v);  // whole unit: no other contributor
+                    float sc[4];
+                    q_scale(unit, sc);
+                    q_store_y(unit, v, sc);  // whole unit: no other contributor
                 } else if (n != nitems - 1) {
                     pend_unit = unit;  // arrival counted after the last item
                     q_publish(unit, v);
