@@ -83,5 +83,39 @@ def build(verbose: bool = True, jobs: int | None = None) -> str:
     return LIB_PATH
 
 
+def build_asan(verbose: bool = True) -> str:
+    """A host-sanitized copy of the library for checking the C11 host code:
+    the host sources compiled by gcc with AddressSanitizer and
+    UndefinedBehaviorSanitizer, linked by g++ (so gcc's runtimes) with the
+    HIP kernel objects of the last build() unchanged, into
+    pyc_amd/lib/asan/libpyc_amd.so. Host code only: nothing of the GPU side is
+    instrumented. Programs linked to it, or a process started with the
+    sanitizer runtimes in LD_PRELOAD, report the first error and stop."""
+    hip, c = sources()
+    missing = [_obj(s) for s in hip if not os.path.exists(_obj(s))]
+    if missing:
+        raise RuntimeError("build() first: the HIP objects are missing")
+    adir = os.path.join(OBJ_DIR, "asan")
+    os.makedirs(adir, exist_ok=True)
+    san = ["-fsanitize=address,undefined", "-fno-omit-frame-pointer", "-g", "-O1"]
+    objs = []
+    for src in c:
+        o = os.path.join(adir, os.path.basename(src) + ".o")
+        _run(["gcc", *[f for f in C_FLAGS if f != "-O2"], *san, "-c", src, "-o", o])
+        objs.append(o)
+    out_dir = os.path.join(LIB_DIR, "asan")
+    os.makedirs(out_dir, exist_ok=True)
+    out = os.path.join(out_dir, "libpyc_amd.so")
+    _run(["g++", "-shared", "-fPIC", "-o", out, *objs, *[_obj(s) for s in hip], "-L", os.path.join(ROCM, "lib"),
+          "-lamdhip64", "-lpthread", "-lm", "-Wl,-Bsymbolic", f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}",
+          "-fsanitize=address,undefined"])
+    if verbose:
+        print(f"built {out} (host code with ASan + UBSan)")
+    return out
+
+
 if __name__ == "__main__":
-    build()
+    if "--asan" in sys.argv[1:]:
+        build_asan()
+    else:
+        build()

@@ -16,6 +16,8 @@ import subprocess
 
 import pytest
 
+ASAN_LIB_DIR = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "pyc_amd", "lib", "asan")
+
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CTEST_DIR = os.path.join(ROOT, "oracle", "_ref", "ctest")
 PROGRAMS = sorted(os.listdir(CTEST_DIR)) if os.path.isdir(CTEST_DIR) else []
@@ -24,13 +26,21 @@ PROGRAMS = sorted(os.listdir(CTEST_DIR)) if os.path.isdir(CTEST_DIR) else []
 NEEDS_SOURCES = {"test_pass_golden"}
 
 
-def _run(name, tmp_path):
+def _run(name, tmp_path, sanitized=False):
     if name in NEEDS_SOURCES and not os.path.isdir("/root/reference/tests/compiler_next/golden"):
         pytest.skip("reads the reference's golden files, which only the build host has")
     env = {k: v for k, v in os.environ.items() if not k.startswith("PYC_")}
+    if sanitized:
+        # the programs find libpyc_amd.so through RUNPATH, which
+        # LD_LIBRARY_PATH overrides; gcc's sanitizer runtimes are preloaded
+        rt = [subprocess.run(["gcc", f"-print-file-name={n}"], capture_output=True, text=True).stdout.strip()
+              for n in ("libasan.so", "libubsan.so")]
+        env.update(LD_LIBRARY_PATH=ASAN_LIB_DIR, LD_PRELOAD=":".join(rt),
+                   ASAN_OPTIONS="detect_leaks=1:halt_on_error=1", UBSAN_OPTIONS="halt_on_error=1:print_stacktrace=1")
     r = subprocess.run([os.path.join(CTEST_DIR, name)], cwd=tmp_path, env=env, capture_output=True, text=True,
                        timeout=120)
     assert r.returncode == 0, f"{name} exited {r.returncode}:\n{r.stdout[-2000:]}\n{r.stderr[-2000:]}"
+    assert "Sanitizer" not in r.stderr and "runtime error" not in r.stderr, r.stderr[-3000:]
     assert "ok" in r.stdout.strip().splitlines()[-1], r.stdout[-500:]
 
 
@@ -38,6 +48,16 @@ def _run(name, tmp_path):
 @pytest.mark.parametrize("name", PROGRAMS)
 def test_reference_ctest(name, tmp_path):
     _run(name, tmp_path)
+
+
+@pytest.mark.skipif(not PROGRAMS or not os.path.exists(os.path.join(ASAN_LIB_DIR, "libpyc_amd.so")),
+                    reason="needs the reference CTest programs and python -m pyc_amd.build --asan")
+@pytest.mark.parametrize("name", PROGRAMS)
+def test_reference_ctest_host_sanitized(name, tmp_path):
+    """The same programs against the host-sanitized library (the C11 host code
+    built with AddressSanitizer, leak checking and UndefinedBehaviorSanitizer):
+    no report may appear."""
+    _run(name, tmp_path, sanitized=True)
 
 
 @pytest.mark.gpu
