@@ -20,6 +20,7 @@
 // layouts ([K,N] tiles are transposed on the LDS store). Waves 0-3 stage B,
 // waves 4-7 stage A.
 #include "common.hpp"
+#include "lds_dma.hpp"
 
 namespace pyc {
 
@@ -188,6 +189,195 @@ gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ B, float*
     }
 }
 
+// Whole-tile form (M, N, K multiples of 64): the same 8-wave 64x64 tile and
+// k-half split, with the operands moved global->LDS by LDS-DMA through a
+// 4-stage ring instead of through VGPRs. Three k-tiles are in flight while
+// the fourth is multiplied, so the HBM/L2 latency (longer than one k-tile's
+// MFMAs, ~2048 cycles per SIMD) is off the critical path; one barrier per
+// k-tile. Each DMA instruction fills 1 KiB of LDS (lane i -> +16 i): four
+// 64-float rows. A (and B as [N,K]) rows keep the k-chunk swizzle of the
+// register-staged kernel (chunk c of row r at c ^ (r & 7)), applied on the
+// global side. B as [K,N] is stored untransposed, [k][n], chunk c of row k at
+// c ^ 4((k >> 2) & 3), and read one element per lane (ds_read_b32): the 16
+// lanes of each k slot read 16 consecutive n of rows 4 apart, which the
+// swizzle puts in four different 16-bank groups.
+constexpr int kF32Stages = 4;
+
+template <bool BT>
+__global__ void __launch_bounds__(512, 1)
+gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,
+                    int M, int N, int K, float alpha, float beta, const float* __restrict__ bias,
+                    int epi, int group_m) {
+    __shared__ __attribute__((aligned(1024))) float smem[kF32Stages * 2 * kF32BM * kF32BK];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int quad = wave & 3;
+    const int kh = wave >> 2;
+    const int wm = quad >> 1;
+    const int wn = quad & 1;
+    // Tile order: workgroups go to the 8 XCDs round robin, so consecutive
+    // tile indices are given to one XCD; tiles are numbered in groups of
+    // group_m tile rows, column by column, so the tiles an XCD holds at once
+    // share a few A row panels and B column panels in its L2.
+    const int tiles_n = N / kF32BN, tiles_m = M / kF32BM;
+    int bid = blockIdx.x;
+    const int nblk = gridDim.x;
+    if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
+    const int span = group_m * tiles_n;
+    const int grp = bid / span;
+    const int first_m = grp * group_m;
+    const int gsz = min(tiles_m - first_m, group_m);
+    const int in = bid - grp * span;
+    const int m0 = (first_m + in % gsz) * kF32BM;
+    const int n0 = (in / gsz) * kF32BN;
+    const int KT = K / kF32BK;
+
+    const i32x4 ra = make_buf_rsrc(A, (uint32_t)((size_t)M * K * 4));
+    const i32x4 rb = make_buf_rsrc(B, (uint32_t)((size_t)N * K * 4));
+    // wave w issues rows 8w .. 8w+7 of the A tile and of the B tile (two
+    // instructions each, four rows per instruction); lane i writes chunk
+    // position p = i % 16 of row 4j + i / 16
+    uint32_t va[2], vb[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int row = 8 * wave + 4 * h + (lane >> 4), p = lane & 15;
+        va[h] = (uint32_t)(((size_t)(m0 + row) * K + 4 * (p ^ (row & 7))) * 4);
+        if constexpr (BT) vb[h] = (uint32_t)(((size_t)(n0 + row) * K + 4 * (p ^ (row & 7))) * 4);
+        else vb[h] = (uint32_t)(((size_t)row * N + n0 + 4 * (p ^ (4 * ((row >> 2) & 3)))) * 4);
+        asm volatile("" : "+v"(va[h]), "+v"(vb[h]));
+    }
+    const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
+    auto issue = [&](int kt) {
+        const uint32_t slot = lds0 + (uint32_t)((kt % kF32Stages) * 2 * kF32BM * kF32BK * 4);
+        const uint32_t sa = (uint32_t)kt * kF32BK * 4;
+        const uint32_t sb = BT ? sa : (uint32_t)kt * kF32BK * (uint32_t)N * 4;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t off = (uint32_t)(8 * wave + 4 * h) * kF32BK * 4;
+            lds_dma_buf_b128_u(ra, va[h], sa, slot + off);
+            lds_dma_buf_b128_u(rb, vb[h], sb, slot + kF32BM * kF32BK * 4 + off);
+        }
+    };
+
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int lrow = lane & 15, lgrp = lane >> 4;
+    // fragments of half kk (16 k: 4 per k slot) of the k-tile in ring slot kt % 4
+    auto frags = [&](int kt, int kk, f32x4 (&af)[2], f32x4 (&bfr)[2]) {
+        const float* As = smem + (kt % kF32Stages) * 2 * kF32BM * kF32BK;
+        const float* Bs = As + kF32BM * kF32BK;
+        const int ch = (kh * 2 + kk) * 4 + lgrp;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int r = wm * 32 + i * 16 + lrow;
+            af[i] = *reinterpret_cast<const f32x4*>(&As[r * kF32BK + swz8(r, ch) * 4]);
+            const int n = wn * 32 + i * 16 + lrow;
+            if constexpr (BT) {
+                bfr[i] = *reinterpret_cast<const f32x4*>(&Bs[n * kF32BK + swz8(n, ch) * 4]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int k = 4 * ch + e;  // (k >> 2) & 3 == lgrp
+                    bfr[i][e] = Bs[k * kF32BN + (((n >> 2) ^ (4 * lgrp)) << 2) + (n & 3)];
+                }
+            }
+        }
+    };
+    auto mma = [&](const f32x4 (&af)[2], const f32x4 (&bfr)[2]) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][e], bfr[j][e], acc[i][j], 0, 0, 0);
+    };
+
+    // Ring: while k-tile kt is multiplied, kt+1 has landed, kt+2 is in flight
+    // and kt+3 is issued into the slot kt-1 left. The first half of k-tile
+    // kt+1's fragments is read during k-tile kt's MFMAs, so the MFMAs after
+    // each barrier do not wait on LDS.
+#pragma unroll
+    for (int s = 0; s < kF32Stages - 1; ++s)
+        if (s < KT) issue(s);
+    // this wave's loads of k-tile t have landed when at most the later issued
+    // k-tiles' (4 loads each) are outstanding
+    if (KT > 2) wait_vmem_le<8>();
+    else if (KT > 1) wait_vmem_le<4>();
+    else wait_vmem_le<0>();
+    __syncthreads();
+    f32x4 af0[2], bf0[2];
+    frags(0, 0, af0, bf0);
+    for (int kt = 0; kt < KT; ++kt) {
+        if (kt + 2 < KT) wait_vmem_le<4>();
+        else wait_vmem_le<0>();
+        // every wave's part of k-tile kt+1 is in LDS, and k-tile kt-1 (and
+        // the prefetch of kt) is consumed
+        __syncthreads();
+        if (kt + kF32Stages - 1 < KT) issue(kt + kF32Stages - 1);
+        // LDS reads of the second half first, then the first half's MFMAs,
+        // the next k-tile's first-half reads (slot kt+1; past the last
+        // k-tile they read a stale slot, unused), the second half's MFMAs
+        constexpr int NRD = BT ? 4 : 6;  // ds_read_b128 + paired ds_read_b32
+        f32x4 af1[2], bf1[2];
+        frags(kt, 1, af1, bf1);
+        mma(af0, bf0);
+        frags(kt + 1, 0, af0, bf0);
+        mma(af1, bf1);
+        __builtin_amdgcn_sched_group_barrier(0x100, NRD, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, NRD, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+    }
+    __syncthreads();  // every wave is done with the ring
+
+    // k halves summed through LDS (waves 4-7 hand theirs to waves 0-3)
+    float* red = smem;
+    if (kh) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) red[(quad * 16 + (i * 2 + j) * 4 + r) * 64 + lane] = acc[i][j][r];
+    }
+    __syncthreads();
+    if (kh) return;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[i][j][r] += red[(quad * 16 + (i * 2 + j) * 4 + r) * 64 + lane];
+
+    const bool has_bias = (epi & 1) && bias != nullptr;
+    const bool relu = (epi & 2) != 0;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int gn = n0 + wn * 32 + j * 16 + lrow;
+        const float bv = has_bias ? bias[gn] : 0.f;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int gm = m0 + wm * 32 + i * 16 + lgrp * 4 + r;
+                float* cp = C + (size_t)gm * N + gn;
+                float v = alpha * acc[i][j][r];
+                if (beta != 0.f) v += beta * *cp;
+                v += bv;
+                if (relu) v = v > 0.f ? v : 0.f;
+                *cp = v;
+            }
+        }
+    }
+}
+
 }  // namespace pyc
 
 extern "C" int pyc_hip_gemm_f32_launch(int b_trans, int M, int N, int K, const void* A,
@@ -200,6 +390,17 @@ extern "C" int pyc_hip_gemm_f32_launch(int b_trans, int M, int N, int K, const v
     const float* a = (const float*)A;
     const float* b = (const float*)B;
     float* c = (float*)C;
+    // the LDS-DMA kernel addresses each operand through a buffer descriptor
+    // (32-bit byte offsets) and moves 16-byte chunks
+    const bool dma = even && K > 0 && (size_t)M * K * 4 < (1ull << 32) && (size_t)N * K * 4 < (1ull << 32) &&
+                     ((uintptr_t)A % 16 == 0) && ((uintptr_t)B % 16 == 0);
+    if (dma) {
+        const dim3 tiles((unsigned)((M / kF32BM) * (N / kF32BN)));
+        const int gm = M / kF32BM < 4 ? M / kF32BM : 4;
+        if (b_trans) hipLaunchKernelGGL((gemm_f32_dma_kernel<true>), tiles, block, 0, s, a, b, c, M, N, K, alpha, beta, bias, epi, gm);
+        else hipLaunchKernelGGL((gemm_f32_dma_kernel<false>), tiles, block, 0, s, a, b, c, M, N, K, alpha, beta, bias, epi, gm);
+        return hipGetLastError() == hipSuccess ? 0 : -2;
+    }
     if (b_trans) {
         if (even) hipLaunchKernelGGL((gemm_f32_kernel<true, false>), grid, block, 0, s, a, b, c, M, N, K, alpha, beta, bias, epi);
         else hipLaunchKernelGGL((gemm_f32_kernel<true, true>), grid, block, 0, s, a, b, c, M, N, K, alpha, beta, bias, epi);

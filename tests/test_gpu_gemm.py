@@ -188,7 +188,9 @@ def test_config1_f32_gemm_bias_relu(gpu):
     assert rel_max_err(Y.cpu().numpy(), ref) <= F32_TOL
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 1, 1), (5, 7, 3), (64, 64, 32), (100, 70, 50), (257, 129, 65)])
+@pytest.mark.parametrize("m,n,k", [(1, 1, 1), (5, 7, 3), (64, 64, 32), (100, 70, 50), (257, 129, 65),
+                                   # whole 64 x 64 x 64 tiles (the LDS-DMA ring): 1, 2, 3 and 5 k-tiles
+                                   (64, 64, 64), (128, 64, 128), (64, 192, 192), (192, 128, 320)])
 @pytest.mark.parametrize("symbol,bt", [("hip_gemm_f32_nn_64x64", False), ("hip_gemm_f32_nt_64x64", True),
                                        ("cutlass_gemm_simt_f32", True),
                                        ("ada_gemm_k64_warp32_async_f32", False)])
@@ -202,6 +204,35 @@ def test_f32_gemm_shapes(gpu, m, n, k, symbol, bt):
     torch.cuda.synchronize()
     ref = oracle.matmul_f32(a, np.ascontiguousarray(b.T) if bt else b)
     assert rel_max_err(Cd.cpu().numpy(), ref) <= F32_TOL
+
+
+@pytest.mark.parametrize("alpha,beta,epi", [(0.5, 0.0, 3), (1.0, 0.0, 2), (-2.0, 0.0, 1), (0.75, 0.5, 3)])
+@pytest.mark.parametrize("symbol,bt", [("hip_gemm_f32_nn_64x64", False), ("hip_gemm_f32_nt_64x64", True)])
+def test_f32_gemm_whole_tile_epilogues(gpu, alpha, beta, epi, symbol, bt):
+    """fp32 C = epi(alpha * A op(B) + beta * C) on whole 64 x 64 x 64 tiles
+    (the LDS-DMA kernel), against the oracle's fp32 matmul; a second launch
+    gives identical bits (fixed k-half summation order)."""
+    torch = gpu
+    m, n, k = 256, 192, 512
+    r = np.random.default_rng(abs(int(alpha * 100)) + epi + 7 * bt)
+    a = r.uniform(-1, 1, (m, k)).astype(np.float32)
+    b = r.uniform(-1, 1, (n, k) if bt else (k, n)).astype(np.float32)
+    c0 = r.uniform(-1, 1, (m, n)).astype(np.float32)
+    bias = r.uniform(-1, 1, n).astype(np.float32)
+    A, B = dev_f32(torch, a), dev_f32(torch, b)
+    outs = []
+    for _ in range(2):
+        Cd = dev_f32(torch, c0.copy())
+        pyc_amd.gemm(symbol, A, B, Cd, m, n, k, alpha=alpha, beta=beta,
+                     bias=dev_f32(torch, bias) if epi & 1 else None, epilogue=epi)
+        torch.cuda.synchronize()
+        outs.append(Cd.cpu().numpy())
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    ref = alpha * oracle.matmul_f32(a, np.ascontiguousarray(b.T) if bt else b) + beta * c0
+    ref = ref + (bias if epi & 1 else 0.0)
+    if epi & 2:
+        ref = np.maximum(ref, 0.0)
+    assert rel_max_err(outs[0], ref) <= F32_TOL
 
 
 def test_reference_symbols_and_rejections(gpu):
