@@ -189,8 +189,11 @@ def test_config1_f32_gemm_bias_relu(gpu):
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 1, 1), (5, 7, 3), (64, 64, 32), (100, 70, 50), (257, 129, 65),
-                                   # whole 64 x 64 x 64 tiles (the LDS-DMA ring): 1, 2, 3 and 5 k-tiles
-                                   (64, 64, 64), (128, 64, 128), (64, 192, 192), (192, 128, 320)])
+                                   # whole 64 x 64 x 64 tiles (the LDS-DMA ring): 1, 2, 3 and 5 k-tiles;
+                                   # 35 tiles (no XCD renumbering, a last tile-row group of one) and
+                                   # 512 tiles (two per CU, renumbered per XCD)
+                                   (64, 64, 64), (128, 64, 128), (64, 192, 192), (192, 128, 320),
+                                   (320, 448, 128), (1024, 2048, 192)])
 @pytest.mark.parametrize("symbol,bt", [("hip_gemm_f32_nn_64x64", False), ("hip_gemm_f32_nt_64x64", True),
                                        ("cutlass_gemm_simt_f32", True),
                                        ("ada_gemm_k64_warp32_async_f32", False)])
