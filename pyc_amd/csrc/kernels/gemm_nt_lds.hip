@@ -608,6 +608,200 @@ gemm_nt_persist_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
     wait_vmem_le<0>();
 }
 
+// ---------------------------------------------------------------------------
+// Tail of a two-round convolution. With 256 x 256 tiles a convolution of
+// between one and two rounds of tiles leaves part of the CUs idle for the
+// whole second round (config 4: 392 tiles on 256 CUs, 120 CUs idle). The
+// launcher then runs one full round of 256-pixel tiles on the persistent
+// kernel and the remaining output pixels here, in tiles of 160 pixels x 256
+// channels, which fit in one round: the second round takes 160/256 of a tile
+// time instead of a whole one.
+// Same implicit-GEMM view, gather and LDS layout as the persistent kernel;
+// one-shot (a workgroup per tile), 4 waves as 2 x 2, each 80 pixels (5
+// fragments) x 128 channels (8 fragments); BK = 64 stages, three in a ring
+// (A 20 KB + B 32 KB each), loaded by LDS-DMA two stages ahead, one barrier
+// per stage, the loads threaded between the MFMAs. Rows past the last pixel
+// gather the last pixel (never stored).
+constexpr int kTailBM = 160;
+constexpr int kTailStages = 3;
+
+template <typename T, int EPI>
+__global__ void __launch_bounds__(256, 1)
+conv_tail_kernel(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, uint16_t* __restrict__ Y,
+                 int m_base, int M, int N, int K, const float* __restrict__ bias, int tiles_n, ConvGeomP cg) {
+    constexpr int BK = 64, CH = 8, NT = 256;
+    constexpr int ROWS_PER_LOAD = kWave / CH;          // 8 rows of 128 bytes per DMA instruction
+    constexpr int ALOADS = kTailBM * CH / NT;          // 5 per wave and stage
+    constexpr int BLOADS = kD_BN * CH / NT;            // 8
+    constexpr int LOADS = ALOADS + BLOADS;             // 13
+    constexpr uint32_t A_BYTES = kTailBM * BK * 2;     // 20 KB
+    constexpr uint32_t STAGE_BYTES = (kTailBM + kD_BN) * BK * 2;
+    constexpr int FM = kTailBM / 2 / 16;               // 5 row fragments per wave
+    static_assert(ALOADS * NT == kTailBM * CH && BLOADS * NT == kD_BN * CH, "DMA split");
+    static_assert(kTailStages * STAGE_BYTES <= 160 * 1024, "LDS");
+    static_assert(4 * (kTailBM / 2) * 128 * 2 <= kTailStages * STAGE_BYTES, "epilogue staging");
+    __shared__ __attribute__((aligned(1024))) uint16_t smem[kTailStages * STAGE_BYTES / 2];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lrow = lane & 15, lgrp = lane >> 4;
+    const int tm = blockIdx.x / tiles_n, tn = blockIdx.x - (blockIdx.x / tiles_n) * tiles_n;
+    const int m0 = m_base + tm * kTailBM;
+    const int n0 = tn * kD_BN;
+    const int ktiles = K / BK;
+
+    const i32x4 a_rsrc = make_buf_rsrc(X, cg.x_bytes);
+    const i32x4 b_rsrc = make_buf_rsrc(Wt, (uint32_t)((size_t)N * K * 2));
+    const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
+
+    // per A row the pixel index of tap (0,0) and its packed input coordinates;
+    // per B row the byte offset of its first chunk
+    uint32_t voff[ALOADS], hw[ALOADS], boff[BLOADS];
+#pragma unroll
+    for (int j = 0; j < ALOADS; ++j) {
+        const int row = (j * 4 + wave) * ROWS_PER_LOAD + lane / CH;
+        const int m = min(m0 + row, M - 1);
+        const int n = m / (cg.P * cg.Q);
+        const int pq = m - n * (cg.P * cg.Q);
+        const int p = pq / cg.Q, q = pq - (pq / cg.Q) * cg.Q;
+        const int ih = p * cg.sh - cg.ph, iw = q * cg.sw - cg.pw;
+        voff[j] = (uint32_t)((n * cg.H + ih) * cg.W + iw);
+        hw[j] = ((uint32_t)(ih + 32768) << 16) | (uint32_t)(iw + 32768);
+    }
+#pragma unroll
+    for (int j = 0; j < BLOADS; ++j) {
+        const int row = (j * 4 + wave) * ROWS_PER_LOAD + lane / CH;
+        boff[j] = (uint32_t)(((size_t)(n0 + row) * K + d_swz(row, lane % CH) * 8) * 2);
+    }
+#pragma unroll
+    for (int j = 0; j < ALOADS; ++j) asm volatile("" : "+v"(voff[j]), "+v"(hw[j]));
+#pragma unroll
+    for (int j = 0; j < BLOADS; ++j) asm volatile("" : "+v"(boff[j]));
+    // a lane's swizzled chunk is the same for every A row it loads (rows differ by multiples of 8)
+    const uint32_t conv_lch = (uint32_t)d_swz(lane / CH, lane % CH) * 8;
+
+    // stage kt: 64 channels from c0 of tap (r, s), channel chunks outside,
+    // taps inside; load j < ALOADS is A row block j, else B row block j - ALOADS
+    struct Tap {
+        int r, s, c0;
+        uint32_t base;
+    };
+    auto tap_of = [&](int kt) {
+        const int ntap = cg.R * cg.S;
+        const int chunk = kt / ntap;
+        const int tap = kt - chunk * ntap;
+        Tap t;
+        t.c0 = chunk * BK;
+        t.r = tap / cg.S;
+        t.s = tap - t.r * cg.S;
+        t.base = lds0 + (uint32_t)(kt % kTailStages) * STAGE_BYTES;
+        return t;
+    };
+    auto dma = [&](int j, const Tap& t) {
+        if (j < ALOADS) {
+            const int ih = (int)(hw[j] >> 16) - 32768 + t.r;
+            const int iw = (int)(hw[j] & 0xFFFFu) - 32768 + t.s;
+            const bool in = ((unsigned)ih < (unsigned)cg.H) & ((unsigned)iw < (unsigned)cg.W);
+            const uint32_t off_in =
+                ((voff[j] + (uint32_t)(t.r * cg.W + t.s)) * (uint32_t)cg.C + (uint32_t)t.c0 + conv_lch) * 2u;
+            const uint32_t off = in ? off_in : 0xFFFFFFF0u;  // past the end of x: reads zeros
+            lds_dma_buf_b128_u(a_rsrc, off, 0u, t.base + (uint32_t)((j * 4 + wave) * ROWS_PER_LOAD * BK * 2));
+        } else {
+            const int jb = j - ALOADS;
+            const uint32_t koff = (uint32_t)(((t.r * cg.S + t.s) * cg.C + t.c0) * 2);
+            lds_dma_buf_b128_u(b_rsrc, boff[jb], koff,
+                               t.base + A_BYTES + (uint32_t)((jb * 4 + wave) * ROWS_PER_LOAD * BK * 2));
+        }
+    };
+
+    f32x4 acc[FM][8];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // Every step issues one stage (clamped to the last: a duplicate into the
+    // free slot), so each wave has exactly two stages of loads outstanding at
+    // the top of a step. Per step, 40 groups of two MFMAs in program order
+    // (sched_barrier): the second k half's fragment reads ride on the first
+    // 13 groups and the 13 DMAs of stage kt+2 on groups 6..18, so neither
+    // stalls the MFMA stream.
+    {
+        const Tap t0 = tap_of(0), t1 = tap_of(min(1, ktiles - 1));
+#pragma unroll
+        for (int j = 0; j < LOADS; ++j) dma(j, t0);
+#pragma unroll
+        for (int j = 0; j < LOADS; ++j) dma(j, t1);
+    }
+    for (int kt = 0; kt < ktiles; ++kt) {
+        wait_vmem_le<LOADS>();  // own loads of stage kt landed (stage kt+1's may be in flight)
+        __syncthreads();        // every wave's part of stage kt is in LDS; stage kt-1 is consumed
+        const Tap tn = tap_of(min(kt + 2, ktiles - 1));
+        const uint16_t* As = smem + (kt % kTailStages) * (STAGE_BYTES / 2);
+        const uint16_t* Bs = As + kTailBM * BK;
+        u32x4 fa[2][FM], fb[2][8];
+        auto rd = [&](int h, int f) {  // fragment f < FM of A, else f - FM of B, k half h
+            const int pc = (h * 4 + lgrp) ^ (lrow & 7);
+            if (f < FM)
+                fa[h][f] = *reinterpret_cast<const u32x4*>(As + (wm * (kTailBM / 2) + 16 * f + lrow) * BK + pc * 8);
+            else
+                fb[h][f - FM] = *reinterpret_cast<const u32x4*>(Bs + (wn * 128 + 16 * (f - FM) + lrow) * BK + pc * 8);
+        };
+#pragma unroll
+        for (int f = 0; f < FM + 8; ++f) rd(0, f);
+#pragma unroll
+        for (int g = 0; g < FM * 8; ++g) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int p = 2 * g + u;         // product p of the step's 2 * FM * 8
+                const int h = p / (FM * 8), q = p % (FM * 8);
+                const int i = q / 8, j = q % 8;
+                acc[i][j] = mfma16x16x32(fb[h][j], fa[h][i], acc[i][j], T{});
+            }
+            if (g < FM + 8) rd(1, g);
+            if (g >= 6 && g < 6 + LOADS) dma(g - 6, tn);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    wait_vmem_le<0>();  // the clamped duplicates have landed too
+    __syncthreads();  // every wave is done with the ring; it becomes the C staging area
+
+    // epilogue: lane's acc[i][j][e] is (pixel 16i + l%16, channel 16j + 4(l/16) + e)
+    // of the wave's 80 x 128 block; staged row-major (256-byte rows, chunk c
+    // of row r at c ^ (r & 15)) and written as whole 256-byte row segments
+    constexpr bool has_bias = (EPI & 1) != 0;
+    constexpr bool relu = (EPI & 2) != 0;
+    uint16_t* stage = smem + wave * ((kTailBM / 2) * 128);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int c = 16 * j + 4 * lgrp;
+        float4 bv = has_bias ? *reinterpret_cast<const float4*>(bias + n0 + wn * 128 + c) : float4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            const int r = 16 * i + lrow;
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[e] = acc[i][j][e] + (&bv.x)[e];
+                if (relu) v[e] = fmaxf(v[e], 0.f);
+            }
+            uint2 packed;
+            packed.x = (uint32_t)elem<T>::from_f32(v[0]) | ((uint32_t)elem<T>::from_f32(v[1]) << 16);
+            packed.y = (uint32_t)elem<T>::from_f32(v[2]) | ((uint32_t)elem<T>::from_f32(v[3]) << 16);
+            *reinterpret_cast<uint2*>(stage + r * 128 + (((c >> 3) ^ (r & 15)) << 3) + (c & 4)) = packed;
+        }
+    }
+#pragma unroll
+    for (int p = 0; p < (kTailBM / 2) / 4; ++p) {
+        const int r = 4 * p + lgrp;
+        const uint4 val = *reinterpret_cast<const uint4*>(stage + r * 128 + ((lrow ^ (r & 15)) << 3));
+        const int gm = m0 + wm * (kTailBM / 2) + r;
+        if (gm < M) *reinterpret_cast<uint4*>(Y + (size_t)gm * N + n0 + wn * 128 + lrow * 8) = val;
+    }
+}
+
 }  // namespace pyc
 
 // Returns 1 when the shape is outside these kernels' preconditions (the caller
@@ -749,7 +943,27 @@ extern "C" int pyc_hip_conv2d_persist_launch(int is_bf16, int Nimg, int H, int W
         else
             n_cu = 256;
     }
-    const int tiles_m = (int)(M / kD_BM), tiles_n = Kout / kD_BN;
+    static int tail_env = -1;
+    if (tail_env < 0) {
+        const char* e = getenv("PYC_CONV_TAIL");
+        tail_env = (e && e[0] == '0') ? 0 : 1;
+    }
+    const int tiles_n = Kout / kD_BN;
+    int tiles_m = (int)(M / kD_BM);
+    // Between one and two rounds of 256-pixel tiles: one full round here and
+    // the remaining pixels in 160-pixel tiles (conv_tail_kernel), when those
+    // fit in one round as well.
+    int m_full = (int)M, tail_tiles = 0;
+    if (tail_env && tiles_m * tiles_n > n_cu && tiles_m * tiles_n <= 2 * n_cu && n_cu / tiles_n > 0 &&
+        ((uintptr_t)bias & 15) == 0) {
+        const int m1 = (n_cu / tiles_n) * kD_BM;
+        const int tm_tail = (int)((M - m1 + kTailBM - 1) / kTailBM);
+        if (tm_tail * tiles_n <= n_cu) {
+            m_full = m1;
+            tiles_m = m1 / kD_BM;
+            tail_tiles = tm_tail * tiles_n;
+        }
+    }
     const int ntiles = tiles_m * tiles_n;
     const ConvGeomP cg{H, W, C, P, Q, R, S, sh, sw, ph, pw, (uint32_t)xb};
     const int epi = ((bias != nullptr) ? 1 : 0) | (relu ? 2 : 0);
@@ -759,7 +973,7 @@ extern "C" int pyc_hip_conv2d_persist_launch(int is_bf16, int Nimg, int H, int W
     const uint16_t* b = (const uint16_t*)w;
     uint16_t* c = (uint16_t*)y;
 #define PYC_CONV(TY, E)                                                                                       \
-    hipLaunchKernelGGL((gemm_nt_persist_kernel<TY, 24, 40, E, true>), grid, block, 0, st, a, b, c, (int)M, Kout, \
+    hipLaunchKernelGGL((gemm_nt_persist_kernel<TY, 24, 40, E, true>), grid, block, 0, st, a, b, c, m_full, Kout, \
                        (int)Kg, 1.0f, bias, tiles_m, tiles_n, 8, cg)
     if (is_bf16) {
         if (epi == 0) PYC_CONV(bf16_t, 0);
@@ -773,5 +987,23 @@ extern "C" int pyc_hip_conv2d_persist_launch(int is_bf16, int Nimg, int H, int W
         else PYC_CONV(f16_t, 3);
     }
 #undef PYC_CONV
+    if (tail_tiles > 0) {
+        const dim3 tgrid(tail_tiles);
+#define PYC_TAIL(TY, E)                                                                                       \
+    hipLaunchKernelGGL((conv_tail_kernel<TY, E>), tgrid, block, 0, st, a, b, c, m_full, (int)M, Kout, (int)Kg, bias, \
+                       tiles_n, cg)
+        if (is_bf16) {
+            if (epi == 0) PYC_TAIL(bf16_t, 0);
+            else if (epi == 1) PYC_TAIL(bf16_t, 1);
+            else if (epi == 2) PYC_TAIL(bf16_t, 2);
+            else PYC_TAIL(bf16_t, 3);
+        } else {
+            if (epi == 0) PYC_TAIL(f16_t, 0);
+            else if (epi == 1) PYC_TAIL(f16_t, 1);
+            else if (epi == 2) PYC_TAIL(f16_t, 2);
+            else PYC_TAIL(f16_t, 3);
+        }
+#undef PYC_TAIL
+    }
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }

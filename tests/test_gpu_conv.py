@@ -104,32 +104,36 @@ def test_conv_reference_abi_and_rejections(gpu):
 
 TILE_CASES = [
     # N, H, W, C, K of a 3x3, pad 1, stride 1 conv on the persistent kernel: tile rounds
-    (8, 56, 56, 256, 256),    # 98 tiles on 256 CUs: one partial round
-    (32, 56, 56, 128, 256),   # 392 tiles of 18 K stages: a full round, then 136 tiles
-    (16, 28, 28, 512, 256),   # 49 tiles of 72 K stages
-    (12, 56, 56, 256, 512),   # 294 tiles, two output-channel tiles per pixel block
+    (8, 56, 56, 256, 256, "bf16"),    # 98 tiles on 256 CUs: one partial round
+    # between one and two rounds: one round of 256-pixel tiles, the rest in
+    # 160-pixel tiles (the tail kernel), the last of them partly past the end
+    (32, 56, 56, 128, 256, "bf16"),   # 392 tiles of 18 K stages -> 256 + 218 tail tiles
+    (16, 28, 28, 512, 256, "bf16"),   # 49 tiles of 72 K stages
+    (12, 56, 56, 256, 512, "bf16"),   # 294 tiles, two output-channel tiles per pixel block -> 256 + 62
+    (24, 56, 56, 256, 256, "f16"),    # 294 tiles -> 256 + 61 tail tiles, fp16
 ]
 
 
-@pytest.mark.parametrize("N,H,W,C,K", TILE_CASES)
-def test_conv_persistent_tile_rounds(gpu, N, H, W, C, K):
+@pytest.mark.parametrize("N,H,W,C,K,dt", TILE_CASES)
+def test_conv_persistent_tile_rounds(gpu, N, H, W, C, K, dt):
     """The persistent implicit-GEMM conv across tile counts below, at and above
     one round of the grid (so workgroups move on to a second tile, through the
-    next-tile prologue). Every output element against a plain PyTorch fp32
-    convolution (an im2col matmul on the device, one image at a time), the
-    first and last images against the oracle, and a second launch gives
-    identical bits."""
+    next-tile prologue, or the remainder goes to the tail kernel). Every output
+    element against a plain PyTorch fp32 convolution (an im2col matmul on the
+    device, one image at a time), the first and last images against the
+    oracle, and a second launch gives identical bits."""
     torch = gpu
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float16
     gx = torch.Generator(device="cuda").manual_seed(N + C)
     gw = torch.Generator(device="cuda").manual_seed(K + 1)
     gb = torch.Generator(device="cuda").manual_seed(K + 2)
-    X = torch.rand((N, H, W, C), generator=gx, device="cuda").to(torch.bfloat16)
-    Wd = (torch.randn((K, 3, 3, C), generator=gw, device="cuda") * np.sqrt(2.0 / (9 * C))).to(torch.bfloat16)
+    X = torch.rand((N, H, W, C), generator=gx, device="cuda").to(tdt)
+    Wd = (torch.randn((K, 3, 3, C), generator=gw, device="cuda") * np.sqrt(2.0 / (9 * C))).to(tdt)
     Bv = 0.01 * torch.randn(K, generator=gb, device="cuda")
-    Y = torch.empty((N, H, W, K), dtype=torch.bfloat16, device="cuda")
+    Y = torch.empty((N, H, W, K), dtype=tdt, device="cuda")
     Y2 = torch.empty_like(Y)
-    pyc_amd.conv2d("hip_conv2d_bf16", X, Wd, Y, pad=(1, 1), stride=(1, 1), bias=Bv, relu=True)
-    pyc_amd.conv2d("hip_conv2d_bf16", X, Wd, Y2, pad=(1, 1), stride=(1, 1), bias=Bv, relu=True)
+    pyc_amd.conv2d(f"hip_conv2d_{dt}", X, Wd, Y, pad=(1, 1), stride=(1, 1), bias=Bv, relu=True)
+    pyc_amd.conv2d(f"hip_conv2d_{dt}", X, Wd, Y2, pad=(1, 1), stride=(1, 1), bias=Bv, relu=True)
     torch.cuda.synchronize()
     assert torch.equal(Y.view(torch.int16), Y2.view(torch.int16))
     kred = 9 * C
@@ -142,9 +146,15 @@ def test_conv_persistent_tile_rounds(gpu, N, H, W, C, K):
         bound = 2.0 ** -8 * ref.abs() + 4e-6 * np.sqrt(kred) * ref.abs().max()
         assert not bool((err > bound).any()), f"image {n}: {int((err > bound).sum())} off"
         assert float(err.max() / ref.abs().max()) <= 2e-2
-    w = oracle.bf16_to_f32(host_bits16(Wd))
     b = Bv.cpu().numpy()
-    for n in (0, N - 1):
-        x = oracle.bf16_to_f32(host_bits16(X[n:n + 1]))
-        ref = oracle.conv2d_nhwc_f32(x, w, b, (1, 1), (1, 1), relu=True)
-        _check(oracle.bf16_to_f32(host_bits16(Y[n:n + 1])), ref, kred)
+    if dt == "bf16":
+        w = oracle.bf16_to_f32(host_bits16(Wd))
+        for n in (0, N - 1):
+            x = oracle.bf16_to_f32(host_bits16(X[n:n + 1]))
+            ref = oracle.conv2d_nhwc_f32(x, w, b, (1, 1), (1, 1), relu=True)
+            _check(oracle.bf16_to_f32(host_bits16(Y[n:n + 1])), ref, kred)
+    else:
+        w = Wd.float().cpu().numpy()
+        for n in (0, N - 1):
+            ref = oracle.conv2d_nhwc_f32(X[n:n + 1].float().cpu().numpy(), w, b, (1, 1), (1, 1), relu=True)
+            _check(Y[n:n + 1].float().cpu().numpy(), ref, kred)

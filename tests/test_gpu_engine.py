@@ -291,12 +291,15 @@ def test_conv_and_attention_modules():
     assert rel_max_err(oracle.bf16_to_f32(out), ref) <= 2e-2
 
 
-def test_conv_module_persistent_graph_replay():
-    """A conv module on the persistent kernel (98 tiles of 256 x 256) through
-    pyc_run_model: three runs (capture, two replays) give identical outputs,
-    which match the oracle on the first and last image."""
+@pytest.mark.parametrize("N", [8, 24])
+def test_conv_module_persistent_graph_replay(N):
+    """A conv module on the persistent kernel through pyc_run_model (8 images:
+    98 tiles of 256 x 256; 24 images: 294 tiles, run as one round of them plus
+    the tail kernel, two launches in the captured graph): three runs (capture,
+    two replays) give identical outputs, which match the oracle on the first
+    and last image."""
     r = np.random.default_rng(9)
-    N, H, W, C, K = 8, 56, 56, 256, 256
+    H, W, C, K = 56, 56, 256, 256
     x = oracle.f32_to_bf16(r.uniform(0, 1, (N, H, W, C)).astype(np.float32))
     w = oracle.f32_to_bf16(r.normal(0, np.sqrt(2.0 / (9 * C)), (K, 3, 3, C)).astype(np.float32))
     ops = [eu.op(abi.OP_INPUT, "x", (N, H, W, C), dtype=abi.DTYPE_BF16),
