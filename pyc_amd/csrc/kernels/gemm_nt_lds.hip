@@ -918,8 +918,8 @@ extern "C" int pyc_hip_gemm_nn_lds_launch(int is_bf16, int M, int N, int K, cons
 
 // Implicit-GEMM NHWC conv2d on the persistent kernel (KRSC filter): returns 1
 // when the shape is outside its preconditions (C % 64 == 0, N*P*Q and K_out
-// multiples of 256, x and w below 4 GiB, 16-byte aligned y), 0 on launch, -2
-// on a launch error.
+// multiples of 256, x and w below 4 GiB, 16-byte aligned y and bias), 0 on
+// launch, -2 on a launch error.
 extern "C" int pyc_hip_conv2d_persist_launch(int is_bf16, int Nimg, int H, int W, int C, int Kout, int R, int S,
                                              int ph, int pw, int sh, int sw, const void* x, const void* w,
                                              const float* bias, int relu, void* y, void* stream) {
@@ -933,6 +933,7 @@ extern "C" int pyc_hip_conv2d_persist_launch(int is_bf16, int Nimg, int H, int W
     const unsigned long long xb = (unsigned long long)Nimg * H * W * C * 2;
     if (xb >= 0xFFFFFFF0ull || (unsigned long long)Kout * Kg * 2 > 0xFFFFFFFFull) return 1;
     if (H >= 32768 || W >= 32768 || ((uintptr_t)y & 15) != 0) return 1;
+    if (bias != nullptr && ((uintptr_t)bias & 15) != 0) return 1;  // the epilogues read bias as float4
     if ((unsigned long long)Nimg * H * W >= (1ull << 31) / (unsigned long long)C) return 1;
     static int n_cu = 0;
     if (n_cu == 0) {
@@ -954,8 +955,7 @@ extern "C" int pyc_hip_conv2d_persist_launch(int is_bf16, int Nimg, int H, int W
     // the remaining pixels in 160-pixel tiles (conv_tail_kernel), when those
     // fit in one round as well.
     int m_full = (int)M, tail_tiles = 0;
-    if (tail_env && tiles_m * tiles_n > n_cu && tiles_m * tiles_n <= 2 * n_cu && n_cu / tiles_n > 0 &&
-        ((uintptr_t)bias & 15) == 0) {
+    if (tail_env && tiles_m * tiles_n > n_cu && tiles_m * tiles_n <= 2 * n_cu && n_cu / tiles_n > 0) {
         const int m1 = (n_cu / tiles_n) * kD_BM;
         const int tm_tail = (int)((M - m1 + kTailBM - 1) / kTailBM);
         if (tm_tail * tiles_n <= n_cu) {

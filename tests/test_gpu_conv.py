@@ -158,3 +158,28 @@ def test_conv_persistent_tile_rounds(gpu, N, H, W, C, K, dt):
         for n in (0, N - 1):
             ref = oracle.conv2d_nhwc_f32(X[n:n + 1].float().cpu().numpy(), w, b, (1, 1), (1, 1), relu=True)
             _check(Y[n:n + 1].float().cpu().numpy(), ref, kred)
+
+
+def test_conv_unaligned_bias_takes_general_kernel(gpu):
+    """A bias that is not 16-byte aligned (a slice one float in) is refused by
+    the persistent and tail kernels, which read it as float4; the general
+    implicit-GEMM kernel runs the same conv and matches the aligned run."""
+    torch = gpu
+    N, H, W, C, K = 4, 32, 32, 64, 256  # 16 whole tiles: persistent-eligible when aligned
+    g = torch.Generator(device="cuda").manual_seed(31)
+    X = torch.rand((N, H, W, C), generator=g, device="cuda").to(torch.bfloat16)
+    Wd = (torch.randn((K, 3, 3, C), generator=g, device="cuda") * np.sqrt(2.0 / (9 * C))).to(torch.bfloat16)
+    Bfull = 0.01 * torch.randn(K + 1, generator=g, device="cuda")
+    Bmis = Bfull[1:]
+    assert Bmis.data_ptr() % 16 != 0
+    Balign = Bmis.clone()
+    Y1 = torch.empty((N, H, W, K), dtype=torch.bfloat16, device="cuda")
+    Y2 = torch.empty_like(Y1)
+    pyc_amd.conv2d("hip_conv2d_bf16", X, Wd, Y1, pad=(1, 1), stride=(1, 1), bias=Bmis, relu=True)
+    pyc_amd.conv2d("hip_conv2d_bf16", X, Wd, Y2, pad=(1, 1), stride=(1, 1), bias=Balign, relu=True)
+    torch.cuda.synchronize()
+    ref = oracle.conv2d_nhwc_f32(oracle.bf16_to_f32(host_bits16(X[:1])), oracle.bf16_to_f32(host_bits16(Wd)),
+                                 Balign.cpu().numpy(), (1, 1), (1, 1), relu=True)
+    _check(oracle.bf16_to_f32(host_bits16(Y1[:1])), ref, 9 * C)
+    d = (Y1.float() - Y2.float()).abs().max().item()
+    assert d <= 2e-2 * Y2.float().abs().max().item()
