@@ -148,10 +148,13 @@ int pyc_hip_kernel_symbol_count(const char* op_key) {
 /* ---------------------------------------------------------------- GEMM */
 
 /* Tile choice for shape-generic symbols: the 256x256 tile when it still gives
- * at least one workgroup per CU (256 CUs on MI355X), else 128x128. */
+ * at least one workgroup per CU (256 CUs on MI355X), else 128x128 when that
+ * gives at least half as many, else 64x64 (small shapes: more workgroups
+ * walking K side by side). */
 static int pick_half_tile(int M, int N) {
     const long t256 = (long)((M + 255) / 256) * (long)((N + 255) / 256);
-    return t256 >= 256 ? 256 : 128;
+    const long t128 = (long)((M + 127) / 128) * (long)((N + 127) / 128);
+    return t256 >= 256 ? 256 : t128 >= 128 ? 128 : 64;
 }
 
 static int gemm_run(const hip_variant* v, int M, int N, int K, const void* A, const void* B,

@@ -70,6 +70,7 @@ extern "C" int pyc_hip_gemm_half_launch(int is_bf16, int b_trans, int tile, int 
     switch (tile) {                                                                              \
         case 256: e = launch_gemm<TY, 256, 256, 2, 2, BT>(A, B, C, M, N, K, alpha, beta, bias, epi, s); break; \
         case 128: e = launch_gemm<TY, 128, 128, 2, 2, BT>(A, B, C, M, N, K, alpha, beta, bias, epi, s); break; \
+        case 64: e = launch_gemm<TY, 64, 64, 2, 2, BT>(A, B, C, M, N, K, alpha, beta, bias, epi, s); break; \
         default: return -1;                                                                      \
     }
     if (is_bf16) {
