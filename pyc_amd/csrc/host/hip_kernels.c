@@ -24,6 +24,8 @@
 int pyc_hip_gemm_half_launch(int is_bf16, int b_trans, int tile, int M, int N, int K,
                              const void* A, const void* B, void* C, float alpha, float beta,
                              const float* bias, int epi, void* stream);
+int pyc_hip_gemm_small_launch(int is_bf16, int b_trans, int M, int N, int K, const void* A, const void* B,
+                              void* C, float alpha, float beta, const float* bias, int epi, void* stream);
 int pyc_hip_gemm_nt_lds_launch(int is_bf16, int M, int N, int K, const void* A, const void* B, void* C,
                                float alpha, float beta, const float* bias, int epi, void* stream);
 int pyc_hip_gemm_nn_lds_launch(int is_bf16, int M, int N, int K, const void* A, const void* B, void* C,
@@ -191,6 +193,15 @@ static int gemm_run(const hip_variant* v, int M, int N, int K, const void* A, co
         }
         if (v->tile == -1) {
             return -1;
+        }
+    }
+    /* Small shapes (64 x 64 tiles): the LDS-DMA ring kernel when the shape
+     * is whole tiles (it answers 1 otherwise). */
+    if (v->tile == 0 && pick_half_tile(M, N) == 64) {
+        const int rc = pyc_hip_gemm_small_launch(v->dtype == VT_BF16, v->b_trans, M, N, K, A, B, C, alpha, beta,
+                                                 bias, epilogue, stream);
+        if (rc != 1) {
+            return rc;
         }
     }
     return pyc_hip_gemm_half_launch(v->dtype == VT_BF16, v->b_trans, v->tile > 0 ? v->tile : pick_half_tile(M, N),

@@ -102,6 +102,51 @@ def test_bf16_nt_lds_more_tiles_than_cus(gpu):
     _check_half(host_bits16(Cd), oracle.gemm_bf16(a, b, True, threads=8), k)
 
 
+@pytest.mark.parametrize("alpha,beta,epi", [(0.5, 0.0, 3), (-2.0, 0.0, 1), (0.75, 0.5, 3)])
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("layout", ["nt", "nn"])
+@pytest.mark.parametrize("m,n,k", [(192, 320, 448), (128, 64, 1024), (64, 64, 64)])
+def test_small_gemm_lds_ring(gpu, alpha, beta, epi, dtype, layout, m, n, k):
+    """Small whole-tile shapes take the 64 x 64 LDS-DMA ring kernel (7, 16 and 1
+    k-steps: a ring that is filled by the prologue, one that wraps twice, and a
+    single step), both B layouts, every epilogue, against the oracle; a second
+    launch gives identical bits."""
+    torch = gpu
+    bt = layout == "nt"
+    r = np.random.default_rng(m + n + k + epi + (7 if bt else 0))
+    a32 = (r.standard_normal((m, k)) / np.sqrt(k)).astype(np.float32)
+    b32 = r.standard_normal((n, k) if bt else (k, n)).astype(np.float32)
+    c32 = r.standard_normal((m, n)).astype(np.float32)
+    bias = r.standard_normal(n).astype(np.float32)
+    sym = f"hip_gemm_{dtype}_{layout}"
+    outs = []
+    for _ in range(2):
+        if dtype == "bf16":
+            a, b, c0 = oracle.f32_to_bf16(a32), oracle.f32_to_bf16(b32), oracle.f32_to_bf16(c32)
+            A, B, Cd = dev_bits16(torch, a), dev_bits16(torch, b), dev_bits16(torch, c0.copy())
+        else:
+            a, b, c0 = a32.astype(np.float16), b32.astype(np.float16), c32.astype(np.float16)
+            A, B, Cd = (torch.from_numpy(x.copy()).cuda() for x in (a, b, c0))
+        pyc_amd.gemm(sym, A, B, Cd, m, n, k, alpha=alpha, beta=beta,
+                      bias=dev_f32(torch, bias) if epi & 1 else None, epilogue=epi)
+        torch.cuda.synchronize()
+        outs.append(Cd.clone())
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    af, bf_ = (a.astype(np.float32), b.astype(np.float32)) if dtype == "f16" else \
+        (oracle.bf16_to_f32(a), oracle.bf16_to_f32(b))
+    prod = oracle.matmul_f32(af, np.ascontiguousarray(bf_.T) if bt else bf_)
+    cin = c0.astype(np.float32) if dtype == "f16" else oracle.bf16_to_f32(c0)
+    ref = alpha * prod + beta * cin + (bias if epi & 1 else 0.0)
+    if epi & 2:
+        ref = np.maximum(ref, 0.0)
+    if dtype == "bf16":
+        _check_half(host_bits16(outs[0]), ref, k)
+    else:
+        got = outs[0].float().cpu().numpy()
+        assert rel_max_err(got, ref) <= BF16_TOL
+        assert np.all(np.abs(got - ref) <= 2.0 ** -10 * np.abs(ref) + 1e-5 * np.sqrt(k) * np.abs(ref).max())
+
+
 @pytest.mark.parametrize("alpha,beta,epi", [(0.5, 0.0, 3), (1.0, 0.0, 2), (-2.0, 0.0, 1), (0.75, 0.5, 3)])
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
 def test_nt_lds_epilogues_full_tiles(gpu, alpha, beta, epi, dtype):
