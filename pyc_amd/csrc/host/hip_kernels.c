@@ -24,8 +24,9 @@
 int pyc_hip_gemm_half_launch(int is_bf16, int b_trans, int tile, int M, int N, int K,
                              const void* A, const void* B, void* C, float alpha, float beta,
                              const float* bias, int epi, void* stream);
-int pyc_hip_gemm_small_launch(int is_bf16, int b_trans, int M, int N, int K, const void* A, const void* B,
-                              void* C, float alpha, float beta, const float* bias, int epi, void* stream);
+int pyc_hip_gemm_small_launch(int is_bf16, int b_trans, int tile, int M, int N, int K, const void* A,
+                              const void* B, void* C, float alpha, float beta, const float* bias, int epi,
+                              void* stream);
 int pyc_hip_gemm_nt_lds_launch(int is_bf16, int M, int N, int K, const void* A, const void* B, void* C,
                                float alpha, float beta, const float* bias, int epi, void* stream);
 int pyc_hip_gemm_nn_lds_launch(int is_bf16, int M, int N, int K, const void* A, const void* B, void* C,
@@ -195,14 +196,14 @@ static int gemm_run(const hip_variant* v, int M, int N, int K, const void* A, co
             return -1;
         }
     }
-    /* Shapes whose 128 x 128 tiles do not fill the chip: the 64 x 64 LDS-DMA
-     * ring kernel when the shape is whole tiles (it answers 1 otherwise);
-     * measured faster there (bf16 1536^3: 46 against 54 us per call), slower
-     * once the 128 x 128 tiles fill every CU. */
-    if (v->tile == 0 && pick_half_tile(M, N) <= 128 &&
-        (long)((M + 127) / 128) * (long)((N + 127) / 128) < 256) {
-        const int rc = pyc_hip_gemm_small_launch(v->dtype == VT_BF16, v->b_trans, M, N, K, A, B, C, alpha, beta,
-                                                 bias, epilogue, stream);
+    /* Below the persistent kernel's range: the LDS-DMA ring kernel when the
+     * shape is whole tiles (it answers 1 otherwise), with 64 x 64 tiles while
+     * 128 x 128 ones would not fill the chip (bf16 1536^3: 46 against 54 us
+     * per call with 128 x 128 tiles), else 128 x 128. */
+    if (v->tile == 0 && pick_half_tile(M, N) <= 128) {
+        const int small = (long)((M + 127) / 128) * (long)((N + 127) / 128) < 256;
+        const int rc = pyc_hip_gemm_small_launch(v->dtype == VT_BF16, v->b_trans, small ? 64 : 128, M, N, K, A, B,
+                                                 C, alpha, beta, bias, epilogue, stream);
         if (rc != 1) {
             return rc;
         }

@@ -105,12 +105,15 @@ def test_bf16_nt_lds_more_tiles_than_cus(gpu):
 @pytest.mark.parametrize("alpha,beta,epi", [(0.5, 0.0, 3), (-2.0, 0.0, 1), (0.75, 0.5, 3)])
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
 @pytest.mark.parametrize("layout", ["nt", "nn"])
-@pytest.mark.parametrize("m,n,k", [(192, 320, 448), (128, 64, 1024), (64, 64, 64)])
+@pytest.mark.parametrize("m,n,k", [(192, 320, 448), (128, 64, 1024), (64, 64, 64),
+                                   (2048, 2048, 256), (1024, 4096, 320)])
 def test_small_gemm_lds_ring(gpu, alpha, beta, epi, dtype, layout, m, n, k):
-    """Small whole-tile shapes take the 64 x 64 LDS-DMA ring kernel (7, 16 and 1
-    k-steps: a ring that is filled by the prologue, one that wraps twice, and a
-    single step), both B layouts, every epilogue, against the oracle; a second
-    launch gives identical bits."""
+    """Whole-tile shapes below the persistent kernel's range take the LDS-DMA
+    ring kernel: 64 x 64 tiles (7, 16 and 1 k-steps: a ring that is filled by
+    the prologue, one that wraps twice, and a single step) and, where 128 x 128
+    tiles fill the chip, 128 x 128 tiles (4 and 5 k-steps through a 4-stage
+    ring); both B layouts, every epilogue, against the oracle; a second launch
+    gives identical bits."""
     torch = gpu
     bt = layout == "nt"
     r = np.random.default_rng(m + n + k + epi + (7 if bt else 0))
