@@ -58,7 +58,7 @@ gemm_small_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B
     const int wm = wave >> 1, wn = wave & 1;
     const int lrow = lane & 15, lgrp = lane >> 4;
     // tiles in groups of 4 tile rows, column by column (neighbouring workgroups share B columns)
-    const int tiles_m = M / BM;
+    const int tiles_m = (M + BM - 1) / BM;
     const int gm = tiles_m < 4 ? tiles_m : 4;
     const int span = gm * tiles_n;
     const int grp = blockIdx.x / span;
@@ -168,12 +168,14 @@ gemm_small_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
         const int gn = n0 + wn * (BN / 2) + 16 * j + 4 * lgrp;
+        if (gn >= N) continue;  // N % 4 == 0: a lane's 4 columns are all in or all out
         float bv[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) bv[e] = has_bias ? bias[gn + e] : 0.f;
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
             const int gm = m0 + wm * (BM / 2) + 16 * i + lrow;
+            if (gm >= M) continue;
             uint16_t* cp = C + (size_t)gm * N + gn;
             float v[4];
             u32x2 old = u32x2{0u, 0u};
@@ -196,18 +198,21 @@ gemm_small_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B
 }  // namespace pyc
 
 // tile: 64 or 128 (square tiles). Returns 1 when the shape is outside this
-// kernel's preconditions (M, N multiples of the tile, K of 64; A, B, C
-// 16-byte aligned; A and B below 4 GiB), 0 on launch, -2 on a launch error.
+// kernel's preconditions (N a multiple of 4, K of 64; A, B, C 16-byte
+// aligned; A and B below 4 GiB), 0 on launch, -2 on a launch error. Ragged M
+// and N: rows of A (and of [N,K] B) past the end are read as zeros through the
+// buffer descriptors, [K,N] B columns past N read neighbouring data, and only
+// the rows and columns of C inside M x N are written.
 extern "C" int pyc_hip_gemm_small_launch(int is_bf16, int b_trans, int tile, int M, int N, int K, const void* A,
                                          const void* B, void* C, float alpha, float beta, const float* bias,
                                          int epi, void* stream) {
     using namespace pyc;
     if (tile != 64 && tile != 128) return 1;
-    if (M <= 0 || N <= 0 || K <= 0 || M % tile || N % tile || K % kSmBK) return 1;
+    if (M <= 0 || N <= 0 || K <= 0 || N % 4 || K % kSmBK) return 1;
     if ((size_t)M * K * 2 > 0xFFFFFFFFull || (size_t)N * K * 2 > 0xFFFFFFFFull) return 1;
     if (((uintptr_t)A | (uintptr_t)B | (uintptr_t)C) & 15) return 1;
-    const int tiles_n = N / tile;
-    const long tiles = (long)(M / tile) * tiles_n;
+    const int tiles_n = (N + tile - 1) / tile;
+    const long tiles = (long)((M + tile - 1) / tile) * tiles_n;
     if (tiles > 0x7FFFFFFFL) return 1;
     hipStream_t s = (hipStream_t)stream;
     const dim3 grid((unsigned)tiles), block(4 * kWave);
