@@ -116,51 +116,76 @@ gemm_small_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B
     const int tr_k = 8 * lgrp + (lrow >> 2);
     const int tr_c = 4 * (lrow & 3);
 
+    // Every step issues one stage, clamped to the last (a duplicate into the
+    // slot the previous step freed), so each wave has STAGES - 2 stages of
+    // loads outstanding at the top of every step. Per step, the MFMAs go out
+    // in program order (sched_barrier) in groups of two, with the second
+    // k-step's fragment reads on the first groups and the DMAs of stage
+    // kt + STAGES - 1 on the following ones, so neither stalls the MFMAs.
+    constexpr int NF = FM + FN;            // fragment reads per k-step
+    constexpr int NG = FM * FN;            // groups of two MFMAs per step (2 k-steps)
+    // the second k-step's MFMAs start at group NG / 2: its fragment reads ride
+    // on the first NF groups when they fit before it, else they go out with
+    // the first k-step's reads (64 x 64 tiles: 4 reads, 2 groups)
+    constexpr bool PRE = NF > NG / 2;
+    constexpr int G_DMA = PRE ? 0 : (NF < NG - LOADS ? NF : NG - LOADS);
+    static_assert(G_DMA + LOADS <= NG && (PRE || NF <= NG / 2), "schedule");
 #pragma unroll
-    for (int s = 0; s < STAGES - 1; ++s)
-        if (s < KT) issue(s);
+    for (int s = 0; s < STAGES - 1; ++s) issue(min(s, KT - 1));
     for (int kt = 0; kt < KT; ++kt) {
-        // own loads of k-step kt landed: the later issued ones (LOADS each) may remain
-        switch (min(STAGES - 2, KT - 1 - kt)) {
-            case 0: wait_vmem_le<0>(); break;
-            case 1: wait_vmem_le<LOADS>(); break;
-            case 2: wait_vmem_le<2 * LOADS>(); break;
-            case 3: wait_vmem_le<3 * LOADS>(); break;
-            case 4: wait_vmem_le<4 * LOADS>(); break;
-            case 5: wait_vmem_le<5 * LOADS>(); break;
-            default: wait_vmem_le<6 * LOADS>(); break;
-        }
-        __syncthreads();  // every wave's part of k-step kt is in LDS; slot kt-1 is consumed
-        if (kt + STAGES - 1 < KT) issue(kt + STAGES - 1);
+        wait_vmem_le<(STAGES - 2) * LOADS>();  // own loads of stage kt landed
+        __syncthreads();  // every wave's part of stage kt is in LDS; slot kt-1 is consumed
+        const int kn = min(kt + STAGES - 1, KT - 1);
+        const uint32_t nslot = lds0 + (uint32_t)((kt + STAGES - 1) % STAGES) * (2 * TILE_BYTES);
+        const uint32_t nsa = (uint32_t)kn * kSmBK * 2;
+        const uint32_t nsb = BT ? nsa : (uint32_t)kn * kSmBK * (uint32_t)N * 2;
         const uint16_t* As = smem + (kt % STAGES) * TILE_BYTES;  // uint16_t units: 2 tiles per stage
         const uint16_t* Bs = As + TILE_BYTES / 2;
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {  // 32 k each
-            u32x4 fa[FM], fb[FN];
-#pragma unroll
-            for (int i = 0; i < FM; ++i) {
-                const int r = wm * (BM / 2) + 16 * i + lrow;
-                fa[i] = *reinterpret_cast<const u32x4*>(As + r * 64 + 8 * ((4 * ks + lgrp) ^ (r & 7)));
-            }
-#pragma unroll
-            for (int j = 0; j < FN; ++j) {
+        u32x4 fa[2][FM], fb[2][FN];
+        auto rd = [&](int ks, int f) {
+            if (f < FM) {
+                const int r = wm * (BM / 2) + 16 * f + lrow;
+                fa[ks][f] = *reinterpret_cast<const u32x4*>(As + r * 64 + 8 * ((4 * ks + lgrp) ^ (r & 7)));
+            } else {
+                const int j = f - FM;
                 if constexpr (BT) {
                     const int r = wn * (BN / 2) + 16 * j + lrow;
-                    fb[j] = *reinterpret_cast<const u32x4*>(Bs + r * 64 + 8 * ((4 * ks + lgrp) ^ (r & 7)));
+                    fb[ks][j] = *reinterpret_cast<const u32x4*>(Bs + r * 64 + 8 * ((4 * ks + lgrp) ^ (r & 7)));
                 } else {
                     const int seg = wn * (SEGS / 2) + j;  // the fragment's 16 columns
                     const int k0 = 32 * ks + tr_k, k1 = k0 + 4;
                     const u32x2 lo = lds_read_tr16(Bs + k0 * BN + 16 * (seg ^ sm_kswz<BN>(k0)) + tr_c);
                     const u32x2 hi = lds_read_tr16(Bs + k1 * BN + 16 * (seg ^ sm_kswz<BN>(k1)) + tr_c);
-                    fb[j] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+                    fb[ks][j] = u32x4{lo[0], lo[1], hi[0], hi[1]};
                 }
             }
+        };
+        auto dma = [&](int d) {  // d < NQ: A, else B
+            const int h = d % NQ;
+            const uint32_t off = (uint32_t)(NQ * wave + h) * 1024;
+            if (d < NQ) lds_dma_buf_b128_u(ra, va[h], nsa, nslot + off);
+            else lds_dma_buf_b128_u(rb, vb[h], nsb, nslot + TILE_BYTES + off);
+        };
 #pragma unroll
-            for (int i = 0; i < FM; ++i)
+        for (int f = 0; f < NF; ++f) rd(0, f);
+        if constexpr (PRE) {
 #pragma unroll
-                for (int j = 0; j < FN; ++j) acc[i][j] = mfma16x16x32(fb[j], fa[i], acc[i][j], T{});
+            for (int f = 0; f < NF; ++f) rd(1, f);
+        }
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int p = 2 * g + u;
+                const int ks = p / (FM * FN), q = p % (FM * FN);
+                acc[q / FN][q % FN] = mfma16x16x32(fb[ks][q % FN], fa[ks][q / FN], acc[q / FN][q % FN], T{});
+            }
+            if (!PRE && g < NF) rd(1, g);
+            if (g >= G_DMA && g < G_DMA + LOADS) dma(g - G_DMA);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
+    wait_vmem_le<0>();  // the clamped duplicates have landed too
 
     // lane's acc[i][j][e] is C[m0 + BM/2 wm + 16 i + lrow][n0 + BN/2 wn + 16 j + 4 lgrp + e]
     const bool has_bias = (epi & 1) && bias != nullptr;
