@@ -249,16 +249,20 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
         asm volatile("" : "+v"(va[h]), "+v"(vb[h]));
     }
     const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
-    auto issue = [&](int kt) {
-        const uint32_t slot = lds0 + (uint32_t)((kt % kF32Stages) * 2 * kF32BM * kF32BK * 4);
+    // DMA d (0..3) of k-tile kt into ring slot `slot`: d / 2 = h, A if d even
+    auto issue_one = [&](int kt, int slot_i, int d) {
+        const uint32_t slot = lds0 + (uint32_t)(slot_i * 2 * kF32BM * kF32BK * 4);
         const uint32_t sa = (uint32_t)kt * kF32BK * 4;
         const uint32_t sb = BT ? sa : (uint32_t)kt * kF32BK * (uint32_t)N * 4;
+        const int h = d >> 1;
+        const uint32_t off = (uint32_t)(8 * wave + 4 * h) * kF32BK * 4;
+        if ((d & 1) == 0) lds_dma_buf_b128_u(ra, va[h], sa, slot + off);
+        else lds_dma_buf_b128_u(rb, vb[h], sb, slot + kF32BM * kF32BK * 4 + off);
+    };
+    // k-tile kt, all four DMAs, into slot kt % 4 (the prologue)
+    auto issue = [&](int kt) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const uint32_t off = (uint32_t)(8 * wave + 4 * h) * kF32BK * 4;
-            lds_dma_buf_b128_u(ra, va[h], sa, slot + off);
-            lds_dma_buf_b128_u(rb, vb[h], sb, slot + kF32BM * kF32BK * 4 + off);
-        }
+        for (int d = 0; d < 4; ++d) issue_one(kt, kt % kF32Stages, d);
     };
 
     f32x4 acc[2][2];
@@ -268,15 +272,17 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
         for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     const int lrow = lane & 15, lgrp = lane >> 4;
-    // fragments of half kk (16 k: 4 per k slot) of the k-tile in ring slot kt % 4
-    auto frags = [&](int kt, int kk, f32x4 (&af)[2], f32x4 (&bfr)[2]) {
+    // fragment f of half kk (16 k: 4 per k slot) of the k-tile in ring slot
+    // kt % 4: f = 0, 1 the A rows 16 f.., f = 2, 3 the B columns 16 (f - 2)..
+    auto rd = [&](int kt, int kk, int f, f32x4 (&af)[2], f32x4 (&bfr)[2]) {
         const float* As = smem + (kt % kF32Stages) * 2 * kF32BM * kF32BK;
         const float* Bs = As + kF32BM * kF32BK;
         const int ch = (kh * 2 + kk) * 4 + lgrp;
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        const int i = f & 1;
+        if (f < 2) {
             const int r = wm * 32 + i * 16 + lrow;
             af[i] = *reinterpret_cast<const f32x4*>(&As[r * kF32BK + swz8(r, ch) * 4]);
+        } else {
             const int n = wn * 32 + i * 16 + lrow;
             if constexpr (BT) {
                 bfr[i] = *reinterpret_cast<const f32x4*>(&Bs[n * kF32BK + swz8(n, ch) * 4]);
@@ -289,52 +295,44 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
             }
         }
     };
-    auto mma = [&](const f32x4 (&af)[2], const f32x4 (&bfr)[2]) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][e], bfr[j][e], acc[i][j], 0, 0, 0);
-    };
 
     // Ring: while k-tile kt is multiplied, kt+1 has landed, kt+2 is in flight
-    // and kt+3 is issued into the slot kt-1 left. The first half of k-tile
-    // kt+1's fragments is read during k-tile kt's MFMAs, so the MFMAs after
-    // each barrier do not wait on LDS.
+    // and kt+3 (clamped to the last k-tile: a duplicate into the free slot)
+    // is issued into the slot kt-1 left, so the wait count is the same every
+    // step. Per step the 32 MFMAs go out in program order (sched_barrier) in
+    // groups of two: the second half's fragment reads ride on the first four
+    // groups, the next k-tile's first-half reads on groups 8-11 (it landed
+    // before this step's barrier), and the four DMAs on groups 12-15.
 #pragma unroll
-    for (int s = 0; s < kF32Stages - 1; ++s)
-        if (s < KT) issue(s);
-    // this wave's loads of k-tile t have landed when at most the later issued
-    // k-tiles' (4 loads each) are outstanding
-    if (KT > 2) wait_vmem_le<8>();
-    else if (KT > 1) wait_vmem_le<4>();
-    else wait_vmem_le<0>();
+    for (int s = 0; s < kF32Stages - 1; ++s) issue(min(s, KT - 1));
+    wait_vmem_le<8>();  // this wave's loads of k-tile 0 landed
     __syncthreads();
     f32x4 af0[2], bf0[2];
-    frags(0, 0, af0, bf0);
+#pragma unroll
+    for (int f = 0; f < 4; ++f) rd(0, 0, f, af0, bf0);
     for (int kt = 0; kt < KT; ++kt) {
-        if (kt + 2 < KT) wait_vmem_le<4>();
-        else wait_vmem_le<0>();
+        wait_vmem_le<4>();  // own loads of k-tile kt+1 landed (kt+2's may be in flight)
         // every wave's part of k-tile kt+1 is in LDS, and k-tile kt-1 (and
         // the prefetch of kt) is consumed
         __syncthreads();
-        if (kt + kF32Stages - 1 < KT) issue(kt + kF32Stages - 1);
-        // LDS reads of the second half first, then the first half's MFMAs,
-        // the next k-tile's first-half reads (slot kt+1; past the last
-        // k-tile they read a stale slot, unused), the second half's MFMAs
-        constexpr int NRD = BT ? 4 : 6;  // ds_read_b128 + paired ds_read_b32
+        const int kn = min(kt + kF32Stages - 1, KT - 1);
         f32x4 af1[2], bf1[2];
-        frags(kt, 1, af1, bf1);
-        mma(af0, bf0);
-        frags(kt + 1, 0, af0, bf0);
-        mma(af1, bf1);
-        __builtin_amdgcn_sched_group_barrier(0x100, NRD, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, NRD, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+#pragma unroll
+        for (int g = 0; g < 16; ++g) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int q = (2 * g + u) & 15;  // MFMA q of the half: element e = q / 4, block (i, j) = q % 4
+                const int e = q >> 2, i = (q >> 1) & 1, j = q & 1;
+                if (g < 8) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af0[i][e], bf0[j][e], acc[i][j], 0, 0, 0);
+                else acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af1[i][e], bf1[j][e], acc[i][j], 0, 0, 0);
+            }
+            if (g < 4) rd(kt, 1, g, af1, bf1);
+            if (g >= 8 && g < 12) rd(kt + 1, 0, g - 8, af0, bf0);  // past the last k-tile: a stale slot, unused
+            if (g >= 12) issue_one(kn, (kt + kF32Stages - 1) % kF32Stages, g - 12);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
+    wait_vmem_le<0>();  // the clamped duplicates have landed too
     __syncthreads();  // every wave is done with the ring
 
     // k halves summed through LDS (waves 4-7 hand theirs to waves 0-3)
