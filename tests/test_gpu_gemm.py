@@ -106,14 +106,14 @@ def test_bf16_nt_lds_more_tiles_than_cus(gpu):
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
 @pytest.mark.parametrize("layout", ["nt", "nn"])
 @pytest.mark.parametrize("m,n,k", [(192, 320, 448), (128, 64, 1024), (64, 64, 64),
-                                   (2048, 2048, 256), (1024, 4096, 320),
+                                   (2048, 2048, 256), (1024, 4096, 320), (2048, 2048, 64),
                                    # ragged M and N (N % 4 == 0): partial tiles, 64 and 128 wide
                                    (100, 196, 128), (2000, 2052, 128)])
 def test_small_gemm_lds_ring(gpu, alpha, beta, epi, dtype, layout, m, n, k):
     """Whole-tile shapes below the persistent kernel's range take the LDS-DMA
     ring kernel: 64 x 64 tiles (7, 16 and 1 k-steps: a ring that is filled by
     the prologue, one that wraps twice, and a single step) and, where 128 x 128
-    tiles fill the chip, 128 x 128 tiles (4 and 5 k-steps through a 4-stage
+    tiles fill the chip, 128 x 128 tiles (4, 5 and 1 k-steps through a 4-stage
     ring); both B layouts, every epilogue, against the oracle; a second launch
     gives identical bits."""
     torch = gpu
