@@ -506,6 +506,7 @@ gemm_nt_persist_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
             for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
         // K loop: same step schedule as gemm_nt_lds4k64_kernel
+        static_assert(GA >= 16 && GA + 16 <= GB && GB >= 32 && GB + 16 <= 64, "event order");
         for (int kt = 0; kt < ktiles; ++kt) {
             const uint32_t cur = (uint32_t)(kt & 1) * (kD_BM * BK);
             const uint32_t nxt = (uint32_t)((kt + 1) & 1) * (kD_BM * BK);
