@@ -188,11 +188,11 @@ __global__ void __launch_bounds__(256) layernorm_kernel(const store_t<T>* __rest
     }
 }
 
-// Rows of at most kLnRegChunks 16-byte chunks per lane (D <= 4096 bf16/fp16,
-// 2048 fp32) whose D is a multiple of 64 chunks: the row is read once into
-// registers, both statistics come from the registers, and it is written once.
-constexpr int kLnRegChunks = 8;
-template <typename T>
+// Rows of at most CAP 16-byte chunks per lane (CAP 8: D <= 4096 bf16/fp16,
+// 2048 fp32; CAP 16 for bf16 and fp32: D <= 8192 bf16, 4096 fp32) whose D is
+// a multiple of 64 chunks: the row is read once into registers, both
+// statistics come from the registers, and it is written once.
+template <typename T, int CAP>
 __global__ void __launch_bounds__(256) layernorm_reg_kernel(const store_t<T>* __restrict__ x,
                                                             const store_t<T>* __restrict__ gamma,
                                                             const store_t<T>* __restrict__ beta,
@@ -204,18 +204,21 @@ __global__ void __launch_bounds__(256) layernorm_reg_kernel(const store_t<T>* __
     if (row >= rows) return;
     const store_t<T>* xr = x + (size_t)row * D;
     store_t<T>* yr = y + (size_t)row * D;
-    const int nc = D / (V * kWave);  // chunks per lane, 1..kLnRegChunks
+    const int nc = D / (V * kWave);  // chunks per lane, 1..CAP
     // bf16 rows stay in registers as raw 16-byte words, unpacked (a shift) at
     // each of their three uses, so all loads go out before the first
     // conversion and the row takes half the registers of unpacked floats; the
     // bf16 path also issues gamma's and beta's loads with the row's (reading
     // the row itself in place of an absent one, so every load is
     // unconditional), which takes their round trip off the end of the row's
-    // work. fp32 needs no unpacking, and for fp16 the compiler keeps the
-    // converted floats live anyway (228 VGPRs), so both keep the floats.
+    // work (at CAP 8; at CAP 16 the row alone takes 64 registers and gamma
+    // and beta are read at the end). fp32 needs no unpacking, and for fp16 the
+    // compiler keeps the converted floats live anyway (228 VGPRs), so both
+    // keep the floats.
     constexpr bool RAW = std::is_same<T, bf16_t>::value;
-    u32x4 raw[RAW ? kLnRegChunks : 1], graw[RAW ? kLnRegChunks : 1], braw[RAW ? kLnRegChunks : 1];
-    float vf[RAW ? 1 : kLnRegChunks][V];
+    constexpr bool PF = RAW && CAP <= 8;
+    u32x4 raw[RAW ? CAP : 1], graw[PF ? CAP : 1], braw[PF ? CAP : 1];
+    float vf[RAW ? 1 : CAP][V];
     auto row_chunk = [&](int j, float (&v)[V]) {
         if constexpr (RAW) IO::unpack(raw[j], v);
         else
@@ -223,16 +226,16 @@ __global__ void __launch_bounds__(256) layernorm_reg_kernel(const store_t<T>* __
             for (int e = 0; e < V; ++e) v[e] = vf[j][e];
     };
 #pragma unroll
-    for (int j = 0; j < kLnRegChunks; ++j)
+    for (int j = 0; j < CAP; ++j)
         if (j < nc) {
             if constexpr (RAW) raw[j] = IO::raw16(xr, (size_t)(j * kWave + lane) * V);
             else IO::get16(xr, (size_t)(j * kWave + lane) * V, vf[j]);
         }
-    if constexpr (RAW) {
+    if constexpr (PF) {
         const store_t<T>* gp = gamma ? gamma : xr;
         const store_t<T>* bp = beta ? beta : xr;
 #pragma unroll
-        for (int j = 0; j < kLnRegChunks; ++j)
+        for (int j = 0; j < CAP; ++j)
             if (j < nc) {
                 graw[j] = IO::raw16(gp, (size_t)(j * kWave + lane) * V);
                 braw[j] = IO::raw16(bp, (size_t)(j * kWave + lane) * V);
@@ -240,7 +243,7 @@ __global__ void __launch_bounds__(256) layernorm_reg_kernel(const store_t<T>* __
     }
     float s = 0.f;
 #pragma unroll
-    for (int j = 0; j < kLnRegChunks; ++j)
+    for (int j = 0; j < CAP; ++j)
         if (j < nc) {
             float v[V];
             row_chunk(j, v);
@@ -250,7 +253,7 @@ __global__ void __launch_bounds__(256) layernorm_reg_kernel(const store_t<T>* __
     const float mean = wave_sum(s) / (float)D;
     float s2 = 0.f;
 #pragma unroll
-    for (int j = 0; j < kLnRegChunks; ++j)
+    for (int j = 0; j < CAP; ++j)
         if (j < nc) {
             float v[V];
             row_chunk(j, v);
@@ -262,12 +265,12 @@ __global__ void __launch_bounds__(256) layernorm_reg_kernel(const store_t<T>* __
         }
     const float rstd = 1.0f / sqrtf(wave_sum(s2) / (float)D + eps);
 #pragma unroll
-    for (int j = 0; j < kLnRegChunks; ++j)
+    for (int j = 0; j < CAP; ++j)
         if (j < nc) {
             const size_t off = (size_t)(j * kWave + lane) * V;
             float v[V], g[V], b[V];
             row_chunk(j, v);
-            if constexpr (RAW) {
+            if constexpr (PF) {
                 IO::unpack(graw[j], g);
                 IO::unpack(braw[j], b);
             } else {
@@ -304,9 +307,13 @@ static int launch_layernorm(const void* x, const void* g, const void* b, void* y
     constexpr int V = io<T>::kVec;
     const bool vec = D % V == 0 && ((((uintptr_t)x | (uintptr_t)y | (uintptr_t)g | (uintptr_t)b) & 15) == 0);
     const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
-    if (vec && D % (V * kWave) == 0 && D / (V * kWave) <= kLnRegChunks)
-        hipLaunchKernelGGL(layernorm_reg_kernel<T>, grid, block, 0, s, (const store_t<T>*)x, (const store_t<T>*)g,
-                           (const store_t<T>*)b, (store_t<T>*)y, rows, D, eps);
+    const int nc = (vec && D % (V * kWave) == 0) ? D / (V * kWave) : 0;  // chunks per lane
+    if (nc >= 1 && nc <= 8)
+        hipLaunchKernelGGL((layernorm_reg_kernel<T, 8>), grid, block, 0, s, (const store_t<T>*)x,
+                           (const store_t<T>*)g, (const store_t<T>*)b, (store_t<T>*)y, rows, D, eps);
+    else if (nc > 8 && nc <= 16 && !std::is_same<T, f16_t>::value)
+        hipLaunchKernelGGL((layernorm_reg_kernel<T, 16>), grid, block, 0, s, (const store_t<T>*)x,
+                           (const store_t<T>*)g, (const store_t<T>*)b, (store_t<T>*)y, rows, D, eps);
     else if (vec)
         hipLaunchKernelGGL((layernorm_kernel<T, true>), grid, block, 0, s, (const store_t<T>*)x,
                            (const store_t<T>*)g, (const store_t<T>*)b, (store_t<T>*)y, rows, D, eps);

@@ -62,10 +62,13 @@ def test_gelu_unaligned(gpu):
 
 @pytest.mark.parametrize("name", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("rows,D,affine,eps", [(257, 1000, False, 1e-5), (64, 4096, True, 1e-5),
-                                               (3, 768, True, 1e-3), (1, 8, True, 1e-5), (130, 5, False, 0.0)])
+                                               (3, 768, True, 1e-3), (1, 8, True, 1e-5), (130, 5, False, 0.0),
+                                               (33, 8192, True, 1e-5), (20, 6144, False, 1e-5)])
 def test_layernorm(gpu, name, rows, D, affine, eps):
     """Rows of mean far from 0 (two-pass variance), D not a multiple of the
-    16-byte chunk (element path), with and without gamma/beta, several eps."""
+    16-byte chunk (element path), with and without gamma/beta, several eps;
+    D = 4096, 6144 and 8192 reach the register-resident kernel's 8- and
+    16-chunk forms (bf16: 8, 12 and 16 chunks per lane)."""
     torch = gpu
     t = _tdtype(torch, name)
     g = torch.Generator(device="cuda").manual_seed(rows * D)
