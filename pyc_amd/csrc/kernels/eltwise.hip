@@ -308,11 +308,12 @@ static int launch_layernorm(const void* x, const void* g, const void* b, void* y
     const bool vec = D % V == 0 && ((((uintptr_t)x | (uintptr_t)y | (uintptr_t)g | (uintptr_t)b) & 15) == 0);
     const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
     const int nc = (vec && D % (V * kWave) == 0) ? D / (V * kWave) : 0;  // chunks per lane
+    constexpr bool kCap16 = !std::is_same<T, f16_t>::value;  // fp16 rows past 8 chunks: three passes
     if (nc >= 1 && nc <= 8)
         hipLaunchKernelGGL((layernorm_reg_kernel<T, 8>), grid, block, 0, s, (const store_t<T>*)x,
                            (const store_t<T>*)g, (const store_t<T>*)b, (store_t<T>*)y, rows, D, eps);
-    else if (nc > 8 && nc <= 16 && !std::is_same<T, f16_t>::value)
-        hipLaunchKernelGGL((layernorm_reg_kernel<T, 16>), grid, block, 0, s, (const store_t<T>*)x,
+    else if (kCap16 && nc > 8 && nc <= 16)
+        hipLaunchKernelGGL((layernorm_reg_kernel<T, kCap16 ? 16 : 8>), grid, block, 0, s, (const store_t<T>*)x,
                            (const store_t<T>*)g, (const store_t<T>*)b, (store_t<T>*)y, rows, D, eps);
     else if (vec)
         hipLaunchKernelGGL((layernorm_kernel<T, true>), grid, block, 0, s, (const store_t<T>*)x,
