@@ -9,12 +9,14 @@ resident operands. Prints ONE JSON line.
 
     python bench.py [--steps K] [--warmup W] [--workload NAME]
 
-The metric names bf16 GEMM and attention, so the default line also carries
-two nested blocks: "attention" (config 3, causal [8,32,2048,128] bf16, with
-its own roofline and CPU baseline) and "engine_cfg1" (config 1 through
-pyc_compile_model/pyc_run_model with device-resident tensors, with the
-reference bench driver's fields under "engine": execution path, profile,
-latency). --no-extras leaves them out.
+The default line also carries one nested block per other BASELINE config,
+each with its own roofline, HBM traffic and CPU baselines (min(cores, 32)
+threads and one thread): "attention" (config 3, causal [8,32,2048,128] bf16),
+"engine_cfg1" (config 1 through pyc_compile_model/pyc_run_model with
+device-resident tensors, with the reference bench driver's fields under
+"engine": execution path, profile, latency), "conv" (config 4, NHWC
+32x56x56x256 -> 256, 3x3, +bias +ReLU) and "decode_chain" (config 5, the
+8-layer fp8-weight chain as hipGraph replays). --no-extras leaves them out.
 
 Other workloads (--workload) measure the remaining BASELINE configs for the
 record; they are not the bench line the driver reads by default. Every line
@@ -457,16 +459,34 @@ def wl_conv(torch, args):
                      "traffic": load_traffic("conv_cfg4"), "kernel_ms": ms_kernel},
     }
     if not args.no_cpu:
+        # The reference's CPU executor has no conv op, so the oracle's direct
+        # convolution is the CPU implementation timed: one image per thread on
+        # min(cores, 32) threads (its C loop runs without the GIL), and one
+        # image on one thread (the reference executor's default thread count).
         import oracle
-        x = X[0:1].float().cpu().numpy()
+        from concurrent.futures import ThreadPoolExecutor
+        threads = min(_host_cores(), 32, N)
+        x = X[0:threads].float().cpu().numpy()
         w = Wd.float().cpu().numpy()
+        bias = Bv.cpu().numpy()
         t0 = time.perf_counter()
-        ref = oracle.conv2d_nhwc_f32(x, w, Bv.cpu().numpy(), (1, 1), (1, 1), True)
+        with ThreadPoolExecutor(threads) as ex:
+            parts = list(ex.map(lambda i: oracle.conv2d_nhwc_f32(x[i:i + 1], w, bias, (1, 1), (1, 1), True),
+                                range(threads)))
         dt = time.perf_counter() - t0
-        res["cpu_baseline"] = {"value": flops / N / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
-                               "sample": f"1 of {N} images, oracle direct conv, {dt:.2f} s, extrapolated linearly"}
-        got = Y[0:1].float().cpu().numpy()
+        ref = np.concatenate(parts, axis=0)
+        res["cpu_baseline"] = {"value": flops * threads / N / dt / 1e12, "unit": "TFLOP/s", "cores": threads,
+                               "kind": "port", "sample": f"{threads} of {N} images, oracle direct conv (fp32), one "
+                                                         f"image per thread, {dt:.2f} s, extrapolated linearly"}
+        t0 = time.perf_counter()
+        oracle.conv2d_nhwc_f32(x[0:1], w, bias, (1, 1), (1, 1), True)
+        dt1 = time.perf_counter() - t0
+        res["cpu_baseline_1thread"] = {"value": flops / N / dt1 / 1e12, "unit": "TFLOP/s", "cores": 1,
+                                       "kind": "port", "sample": f"1 of {N} images on 1 thread, {dt1:.2f} s, "
+                                                                 "extrapolated linearly"}
+        got = Y[0:threads].float().cpu().numpy()
         res["parity_sample_max_rel_err"] = float(np.abs(got - ref).max() / np.abs(ref).max())
+        res["speedup_vs_cpu"] = res["value"] / res["cpu_baseline"]["value"]
     return res
 
 
@@ -580,6 +600,9 @@ def wl_engine_cfg1(torch, args):
     if not args.no_cpu:
         cpu, _ = cpu_baseline_gemm(x, w, flops, "full config-1 GEMM (bias+ReLU not timed)")
         res["cpu_baseline"] = cpu
+        cpu1, _ = cpu_baseline_gemm(x[:256], w, flops, "256 of 1024 rows of the config-1 GEMM, 1 thread",
+                                    threads=1)
+        res["cpu_baseline_1thread"] = cpu1
     return res
 
 
@@ -705,7 +728,7 @@ def main() -> int:
                     help="rows of the GEMM the CPU executor computes (about 10-30 CPU-seconds)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
-                    help="default workload only: skip the nested attention and engine blocks")
+                    help="default workload only: skip the nested config 1, 3, 4 and 5 blocks")
     ap.add_argument("--settle-ms", type=float, default=400.0,
                     help="untimed back-to-back launches before the warmup steps (clock ramp)")
     args = ap.parse_args()
@@ -737,6 +760,15 @@ def main() -> int:
         nested["attention"] = att
         eng = wl_engine_cfg1(torch, args)
         nested["engine_cfg1"] = eng
+        # configs 4 and 5, each with its own roofline, traffic and both CPU
+        # legs: the conv (MFMA-bound) and the decode chain (HBM-bound, timed
+        # as hipGraph replays of the whole 16-step chain)
+        for name, fn in (("conv", wl_conv), ("decode_chain", wl_decode_chain)):
+            blk = fn(torch, args)
+            blk["latency_ms"] = dict(_LAST_LATENCY)
+            blk["settle"] = dict(_LAST_SETTLE)
+            nested[name] = blk
+            torch.cuda.empty_cache()
     line = {
         "metric": METRIC, "value": res["value"], "unit": res["unit"], "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": True,

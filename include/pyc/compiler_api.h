@@ -128,8 +128,9 @@ typedef struct {
     double graph_exec_ms;
     double controller_ms;
     double kernel_select_ms;
-    /* GPU timings keep their cuda_ names; on this build cuda_kernel_ms is
-     * device time between HIP events, not host launch time. */
+    /* GPU timings keep their cuda_ names. cuda_kernel_ms is the host time of
+     * the kernel enqueue, as in the reference; with PYC_HIP_KERNEL_EVENTS=1
+     * it is the device time between HIP events around the run's work. */
     double cuda_copy_in_ms;
     double cuda_kernel_ms;
     double cuda_copy_out_ms;
@@ -178,6 +179,8 @@ typedef struct pyc_compiled_model pyc_compiled_model;
 const char* pyc_status_string(pyc_status status);
 pyc_status pyc_compile_model(const pyc_model_desc* desc, const pyc_compile_options* options, pyc_compiled_model** out_model);
 pyc_status pyc_run_model(pyc_compiled_model* model, const pyc_tensor* inputs, size_t input_count, pyc_tensor* outputs, size_t output_count, pyc_run_stats* out_stats);
+/* Thread-safe against other readers of the same model; must not overlap a
+ * pyc_run_model of that model (the run rewrites the log it returns). */
 const char* pyc_model_last_decision_log(const pyc_compiled_model* model);
 /* Always NULL on this single-GPU build. */
 const pyc_collective_comm* pyc_model_distributed_comm(const pyc_compiled_model* model);

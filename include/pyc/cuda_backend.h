@@ -23,8 +23,10 @@ typedef enum {
 
 #define PYC_CUDA_REASON_MAX 128
 
-/* reference cuda_backend.h:45-55. On this build kernel_ms is device time
- * between HIP events around the kernels, sync_ms the host wait. */
+/* reference cuda_backend.h:45-55. kernel_ms is, as in the reference, the
+ * host time spent enqueueing the run's kernels (or its graph launch); with
+ * PYC_HIP_KERNEL_EVENTS=1 it is instead the device time between HIP events
+ * recorded around the run's work. sync_ms is the host wait for completion. */
 typedef struct {
     int  cuda_requested;
     int  cuda_available;

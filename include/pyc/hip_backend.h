@@ -65,7 +65,15 @@ int pyc_hip_attention_dispatch(
 /* Generalises reference conv2d/kernel.cu:80-112 with a fused epilogue:
  * y[n,p,q,k] = relu?(bias[k] + sum_{r,s,c} x[n,p*sh-ph+r,q*sw-pw+s,c] w[k,r,s,c]),
  * x NHWC, w KRSC, y NPQK; out-of-image taps read zero. bias may be NULL.
- * Symbol "hip_conv2d_bf16" (bf16) or "hip_conv2d_f16". C_in % 8 == 0. */
+ * C_in % 8 == 0. The symbol fixes the element type and the kernel path:
+ *   hip_conv2d_bf16 / _f16          by shape: whole 256 x 256 tiles on the
+ *                                   persistent kernel, a second partial round
+ *                                   on 160-pixel tail tiles, else the tiles below
+ *   hip_conv2d_bf16_persist / _f16_persist   every tile on the persistent kernel
+ *                                   (no tail kernel), else the tiles below
+ *   hip_conv2d_bf16_tiled / _f16_tiled       the register-staged implicit-GEMM
+ *                                   tiles (256 x 256 when they fill the chip, else 128)
+ * All three give the same results up to fp32 summation order. */
 int pyc_hip_conv2d_dispatch(
     const char* symbol,
     int N, int H, int W, int C_in,
@@ -178,8 +186,42 @@ typedef struct {
 /* Returns 0 and fills info for the current device, -1 when no HIP device. */
 int pyc_hip_device_query(pyc_hip_device_info* info);
 
+/* Measured choice between the conv2d paths above at a live shape: every
+ * registered conv2d variant of `dtype` (PYC_DTYPE_BF16/F16) is timed as in
+ * pyc_hip_autotune_gemm (scratch operands of uniform [0,1) activations and
+ * [-1,1) weights, bias and ReLU on, settle, three interleaved rounds of
+ * `iters` launches); the fastest median becomes the symbol the backend plans
+ * for conv2d steps of that dtype and geometry. Outputs and return value as
+ * pyc_hip_autotune_gemm. */
+int pyc_hip_autotune_conv2d(
+    pyc_dtype dtype, int N, int H, int W, int C_in, int K, int R, int S,
+    int pad_h, int pad_w, int stride_h, int stride_w, int iters,
+    char* syms, size_t sym_stride, double* ms, int cap);
+
+/* Resources of the kernel a registered symbol launches (at the large shapes
+ * its registry entry describes; shape-chosen symbols may launch another kernel
+ * for small shapes). The registry's shared_mem_bytes and
+ * estimated_occupancy (waves_per_simd / 8) are the compiled-in figures;
+ * with a HIP device present the attr_* fields are read from the loaded code
+ * object (hipFuncGetAttributes, hipOccupancyMaxActiveBlocksPerMultiprocessor)
+ * and device is 1. Returns 0, or -1 for an unknown symbol. */
+typedef struct {
+    char kernel[64];           /* kernel (template instance) name */
+    size_t lds_bytes;          /* LDS per workgroup, as registered */
+    int threads;               /* workgroup size */
+    int waves_per_simd;        /* resident waves per SIMD, as registered */
+    int device;                /* 1 when the attr_ fields are filled */
+    size_t attr_lds_bytes;     /* sharedSizeBytes (all LDS here is static) */
+    int attr_regs;             /* numRegs */
+    size_t attr_scratch_bytes; /* localSizeBytes: spill per lane */
+    int attr_max_threads;      /* maxThreadsPerBlock (launch bounds) */
+    int attr_blocks_per_cu;    /* resident workgroups per CU at `threads` */
+} pyc_hip_kernel_resources;
+int pyc_hip_kernel_resources_query(const char* symbol, pyc_hip_kernel_resources* out);
+
 /* Number of kernel symbols compiled into this library for op_key
- * ("matmul", "attention", "conv2d", "matmul_w8a16"), independent of the
+ * ("matmul", "attention", "conv2d", "matmul_w8a16", "matmul_w8a16_chain",
+ * "gelu", "layernorm"), independent of the
  * registry's state. */
 int pyc_hip_kernel_symbol_count(const char* op_key);
 

@@ -59,6 +59,12 @@ def _declare(L: C.CDLL) -> None:
     L.pyc_hip_layernorm_dispatch.restype = I
     L.pyc_hip_device_query.argtypes = [C.POINTER(abi.DeviceInfo)]
     L.pyc_hip_device_query.restype = I
+    L.pyc_hip_kernel_resources_query.argtypes = [S, C.POINTER(abi.KernelResources)]
+    L.pyc_hip_kernel_resources_query.restype = I
+    L.pyc_hip_autotune_gemm.argtypes = [I, I, I, I, I, C.c_char_p, Z, C.POINTER(C.c_double), I]
+    L.pyc_hip_autotune_gemm.restype = I
+    L.pyc_hip_autotune_conv2d.argtypes = [I] + [I] * 11 + [I, C.c_char_p, Z, C.POINTER(C.c_double), I]
+    L.pyc_hip_autotune_conv2d.restype = I
     L.pyc_hip_kernel_symbol_count.argtypes = [S]
     L.pyc_hip_kernel_symbol_count.restype = I
     L.pyc_cutlass_kernel_count.argtypes = [S]
@@ -222,3 +228,37 @@ def device_info() -> abi.DeviceInfo:
     info = abi.DeviceInfo()
     _check(lib().pyc_hip_device_query(C.byref(info)), "device query")
     return info
+
+
+def kernel_resources(symbol: str) -> abi.KernelResources:
+    """The registered LDS / waves-per-SIMD figures of the kernel a symbol
+    launches, and (with a device) the loaded code object's own figures."""
+    r = abi.KernelResources()
+    _check(lib().pyc_hip_kernel_resources_query(_b(symbol), C.byref(r)), f"kernel resources {symbol}")
+    return r
+
+
+def _tune_out(n, names, ms):
+    return [(names[i * 64:(i + 1) * 64].split(b"\0", 1)[0].decode(), ms[i]) for i in range(max(n, 0))]
+
+
+def autotune_gemm(dtype: int, M: int, N: int, K: int, iters: int = 10):
+    """pyc_hip_autotune_gemm: [(symbol, median ms)] of every timed variant."""
+    names = C.create_string_buffer(64 * 16)
+    ms = (C.c_double * 16)()
+    n = lib().pyc_hip_autotune_gemm(dtype, M, N, K, iters, names, 64, ms, 16)
+    if n < 0:
+        raise PycError(f"autotune gemm failed with status {n}")
+    return _tune_out(n, names.raw, ms)
+
+
+def autotune_conv2d(dtype: int, N: int, H: int, W: int, C_in: int, K: int, R: int, S: int, pad=(1, 1),
+                    stride=(1, 1), iters: int = 10):
+    """pyc_hip_autotune_conv2d: [(symbol, median ms)] of every timed conv path."""
+    names = C.create_string_buffer(64 * 16)
+    ms = (C.c_double * 16)()
+    n = lib().pyc_hip_autotune_conv2d(dtype, N, H, W, C_in, K, R, S, pad[0], pad[1], stride[0], stride[1], iters,
+                                      names, 64, ms, 16)
+    if n < 0:
+        raise PycError(f"autotune conv2d failed with status {n}")
+    return _tune_out(n, names.raw, ms)

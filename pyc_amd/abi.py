@@ -258,6 +258,22 @@ class DeviceInfo(C.Structure):
     ]
 
 
+class KernelResources(C.Structure):
+    """pyc_hip_kernel_resources (pyc/hip_backend.h)."""
+    _fields_ = [
+        ("kernel", C.c_char * 64),
+        ("lds_bytes", C.c_size_t),
+        ("threads", C.c_int),
+        ("waves_per_simd", C.c_int),
+        ("device", C.c_int),
+        ("attr_lds_bytes", C.c_size_t),
+        ("attr_regs", C.c_int),
+        ("attr_scratch_bytes", C.c_size_t),
+        ("attr_max_threads", C.c_int),
+        ("attr_blocks_per_cu", C.c_int),
+    ]
+
+
 CPU_EXECUTOR_FN = C.CFUNCTYPE(C.c_int, C.POINTER(IrModule), C.POINTER(Tensor), C.c_size_t,
                               C.POINTER(Tensor), C.c_size_t, C.c_void_p)
 

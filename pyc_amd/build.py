@@ -8,6 +8,12 @@ Usage: ``python -m pyc_amd.build`` (or ``__graft_entry__.build()``).
 * ``csrc/host/*.c`` are compiled as C11 by gcc against the HIP runtime C API.
 * Everything links into one in-tree shared library, ``pyc_amd/lib/libpyc_amd.so``,
   whose exported C-ABI is declared in ``include/pyc/*.h``.
+* The same objects, without the engine (compiler_api, ir, pass_manager,
+  runtime_allocator, runtime_control) and without the kernel registry, also
+  link into ``pyc_amd/lib/libpyc_amd_backend.so``: the GPU backend alone, for
+  a program that keeps its own engine (the reference's). Its registry calls
+  (``pyc_kernel_register`` and the rest) are left undefined, so they bind to
+  the registry of the program that loads it.
 """
 from __future__ import annotations
 
@@ -25,6 +31,10 @@ HIPCC = os.path.join(ROCM, "bin", "hipcc")
 OBJ_DIR = os.path.join(HERE, "_build")
 LIB_DIR = os.path.join(HERE, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libpyc_amd.so")
+BACKEND_LIB_PATH = os.path.join(LIB_DIR, "libpyc_amd_backend.so")
+# host sources of the backend-only library: the dispatch, the kernel entry
+# points and the op helpers the lowering uses
+BACKEND_HOST = ("hip_backend.c", "hip_kernels.c", "cpu_ops.c")
 ARCH = "gfx950"
 
 HIP_FLAGS = [
@@ -78,8 +88,14 @@ def build(verbose: bool = True, jobs: int | None = None) -> str:
           *[_obj(s) for s in hip + c], "-L", os.path.join(ROCM, "lib"), "-lamdhip64",
           "-lpthread", "-lm", "-Wl,-Bsymbolic", f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}"])
     shutil.move(tmp, LIB_PATH)
+    tmp = BACKEND_LIB_PATH + ".tmp"
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp,
+          *[_obj(s) for s in hip + [x for x in c if os.path.basename(x) in BACKEND_HOST]],
+          "-L", os.path.join(ROCM, "lib"), "-lamdhip64", "-lpthread", "-lm", "-Wl,-Bsymbolic",
+          f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}"])
+    shutil.move(tmp, BACKEND_LIB_PATH)
     if verbose:
-        print(f"built {LIB_PATH} ({len(hip)} HIP + {len(c)} C sources)")
+        print(f"built {LIB_PATH} ({len(hip)} HIP + {len(c)} C sources) and {os.path.basename(BACKEND_LIB_PATH)}")
     return LIB_PATH
 
 

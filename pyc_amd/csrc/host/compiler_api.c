@@ -19,8 +19,12 @@
  *     on the GPU the backend fuses bias/ReLU into the kernel epilogue instead;
  *   - the CPU executor's ADD broadcasts a [N] or [1] operand over rows (the
  *     reference's flat add reads past the end of a bias, compiler_api.c:1974-2015);
- *   - on the GPU backend the autotune record of a run is the measured device
- *     time of the symbol that ran (trace kernel_ms), not a heuristic estimate;
+ *   - on the GPU backend enable_autotune times every registered GEMM and
+ *     conv2d variant at the module's live shapes on the device
+ *     (measured_autotune) instead of recording one estimated candidate per
+ *     run; where nothing was measured, the per-run record is the device time
+ *     of the run when the backend's HIP events are on (PYC_HIP_KERNEL_EVENTS=1)
+ *     and the reference's estimate otherwise;
  *   - PYC_HIP_STRICT=1 turns any CPU fallback of the GPU backend into
  *     PYC_STATUS_RUNTIME_FAILED (used by the parity tests and the bench);
  *   - no communicator is ever created (single GPU): distributed options are
@@ -977,6 +981,85 @@ static int autotune_persist(const char* path, const char* op, pyc_backend backen
     return rc;
 }
 
+/* The conv2d half of measured_autotune: every registered conv2d path of each
+ * distinct convolution of the module (NHWC x [N,H,W,C] and KRSC w [K,R,S,C]
+ * inputs, stride and padding from the op name) is timed at its live geometry
+ * (pyc_hip_autotune_conv2d), which makes the fastest the planned symbol for
+ * that geometry; each result updates the registry's "conv2d" entry and is
+ * persisted as a `conv2d|backend|symbol|best_ms` line, and the winner of the
+ * largest convolution (by output elements x K) is promoted. */
+static void measured_autotune_conv(pyc_compiled_model* model, const pyc_ir_module* m) {
+    enum { MAX_SHAPES = 8 };
+    char syms[8][PYC_KERNEL_SYMBOL_MAX];
+    char promote[PYC_KERNEL_SYMBOL_MAX] = "";
+    double ms[8];
+    double promote_work = -1.0;
+    int seen[MAX_SHAPES][12];
+    size_t nseen = 0;
+    size_t i;
+    int n, j, best;
+    for (i = 0; i < m->op_count; ++i) {
+        const pyc_ir_op* op = &m->ops[i];
+        const pyc_ir_op *x, *w;
+        int key[12];
+        size_t k;
+        int dup = 0;
+        if (op->kind != PYC_IR_OP_CONV2D || op->input_count < 2 || op->input_ids[0] < 0 || op->input_ids[1] < 0 ||
+            (size_t)op->input_ids[0] >= m->op_count || (size_t)op->input_ids[1] >= m->op_count) {
+            continue;
+        }
+        x = &m->ops[op->input_ids[0]];
+        w = &m->ops[op->input_ids[1]];
+        if (x->shape.rank != 4 || w->shape.rank != 4 || x->shape.dims[3] != w->shape.dims[3] || x->dtype != w->dtype ||
+            (x->dtype != PYC_DTYPE_BF16 && x->dtype != PYC_DTYPE_F16)) {
+            continue;
+        }
+        memset(key, 0, sizeof(key));
+        key[0] = (int)x->dtype;
+        key[1] = (int)x->shape.dims[0];
+        key[2] = (int)x->shape.dims[1];
+        key[3] = (int)x->shape.dims[2];
+        key[4] = (int)x->shape.dims[3];
+        key[5] = (int)w->shape.dims[0];
+        key[6] = (int)w->shape.dims[1];
+        key[7] = (int)w->shape.dims[2];
+        pyc_op_conv_attrs(op->name, &key[10], &key[11], &key[8], &key[9]);
+        for (k = 0; k < nseen; ++k) {
+            dup |= memcmp(seen[k], key, sizeof(key)) == 0;
+        }
+        if (dup || nseen == MAX_SHAPES) {
+            continue;
+        }
+        memcpy(seen[nseen++], key, sizeof(key));
+        n = pyc_hip_autotune_conv2d((pyc_dtype)key[0], key[1], key[2], key[3], key[4], key[5], key[6], key[7], key[8],
+                                    key[9], key[10], key[11], 10, &syms[0][0], PYC_KERNEL_SYMBOL_MAX, ms, 8);
+        if (n <= 0) {
+            continue;
+        }
+        best = 0;
+        for (j = 0; j < n; ++j) {
+            (void)pyc_kernel_benchmark_update_symbol("conv2d", model->backend, syms[j], ms[j]);
+            if (autotune_persist(model->autotune_db, "conv2d", model->backend, syms[j], ms[j]) == 0) {
+                model->autotune_saved = 1;
+            }
+            if (ms[j] < ms[best]) {
+                best = j;
+            }
+        }
+        {
+            const double work = (double)key[1] * key[2] * key[3] * key[5] * key[6] * key[7] * key[4];
+            if (work > promote_work) {
+                promote_work = work;
+                copy_str(promote, sizeof(promote), syms[best]);
+            }
+        }
+        model->hip_tuned = 1;
+    }
+    if (promote[0]) {
+        (void)pyc_kernel_promote_symbol("conv2d", model->backend, promote);
+    }
+}
+
 /* On the GPU backend the first run with enable_autotune measures every
  * registered tile variant of each distinct [M,K]x[K,N] GEMM shape of the
  * module at its live shape (pyc_hip_autotune_gemm, HIP-event timings), which
@@ -1045,6 +1128,7 @@ static void measured_autotune(pyc_compiled_model* model, const pyc_ir_module* m)
     if (promote[0]) {
         (void)pyc_kernel_promote_symbol("matmul", model->backend, promote);
     }
+    measured_autotune_conv(model, m);
 }
 
 /* Heuristic time of a not-measured candidate (reference compiler_api.c:562-589);
@@ -1384,9 +1468,11 @@ static int execute_cpu_graph(const pyc_ir_module* m, const pyc_tensor* inputs, s
                                     conv[6], conv[7], conv[8], conv[9], conv[10]);
                 break;
             case PYC_IR_OP_ATTENTION:
-                pyc_cpu_attention(val[a], val[b], val[c3], out, (int)shp[a].dims[0], (int)shp[a].dims[1],
-                                  (int)shp[a].dims[2], (int)shp[a].dims[3], pyc_op_is_causal(op->name),
-                                  1.0f / sqrtf((float)shp[a].dims[3]));
+                if (pyc_cpu_attention(val[a], val[b], val[c3], out, (int)shp[a].dims[0], (int)shp[a].dims[1],
+                                      (int)shp[a].dims[2], (int)shp[a].dims[3], pyc_op_is_causal(op->name),
+                                      1.0f / sqrtf((float)shp[a].dims[3])) != 0) {
+                    fail = 1;
+                }
                 break;
             default:
                 break;
@@ -1834,9 +1920,12 @@ pyc_status pyc_run_model(pyc_compiled_model* model, const pyc_tensor* inputs, si
         } else {
             copy_str(cand.symbol, sizeof(cand.symbol), "matmul_cpu_ref");
         }
-        if (model->backend == PYC_BACKEND_CUDA && model->trace.kernel_ms > 0.0 && !model->trace.fallback_to_cpu) {
-            ms = model->trace.kernel_ms; /* measured device time */
+        if (model->backend == PYC_BACKEND_CUDA && env_on("PYC_HIP_KERNEL_EVENTS") && model->trace.kernel_ms > 0.0 &&
+            !model->trace.fallback_to_cpu) {
+            ms = model->trace.kernel_ms; /* device time between the backend's HIP events */
         } else {
+            /* the reference's estimate; without the events kernel_ms is the
+             * host time of the enqueue, which is no kernel time */
             ms = estimate_ms(run_ms > 0.0 ? run_ms : (dispatch_ms > 0.0 ? dispatch_ms : 0.001), &cand,
                              model->options.objective_mode, st.pressure_score);
         }
@@ -1931,13 +2020,21 @@ pyc_status pyc_run_model(pyc_compiled_model* model, const pyc_tensor* inputs, si
     return error ? PYC_STATUS_RUNTIME_FAILED : PYC_STATUS_OK;
 }
 
+/* The run's log is formatted on the first read after the run. Readers of one
+ * model are serialised by g_log_lock, so two threads reading the same model's
+ * log see one formatting; as in the reference (whose pyc_run_model writes the
+ * log text itself), a read must not overlap a pyc_run_model of that model. */
+static pyc_mutex g_log_lock = PYC_MUTEX_INIT;
+
 const char* pyc_model_last_decision_log(const pyc_compiled_model* model) {
     if (!model) {
         return "";
     }
+    pyc_mutex_lock(&g_log_lock);
     if (model->runlog.pending) {
         run_log_format((pyc_compiled_model*)model); /* the handle is the caller's mutable model */
     }
+    pyc_mutex_unlock(&g_log_lock);
     return model->log;
 }
 

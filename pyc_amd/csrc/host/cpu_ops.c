@@ -270,14 +270,15 @@ typedef struct {
     float* o;
     int S, D, causal;
     float scale;
+    float* rows;    /* one score row of S floats per thread's range */
+    size_t per;     /* heads per range (the range of head lo is lo / per) */
 } attn_ctx;
 
 static void attn_heads(void* p, size_t lo, size_t hi) {
     const attn_ctx* a = (const attn_ctx*)p;
     const int S = a->S, D = a->D;
-    float* sc = (float*)malloc((size_t)S * sizeof(float));
+    float* sc = a->rows + (lo / a->per) * (size_t)S;
     size_t bh;
-    if (!sc) return;
     for (bh = lo; bh < hi; ++bh) {
         const float* qb = a->q + bh * (size_t)S * D;
         const float* kb = a->k + bh * (size_t)S * D;
@@ -311,11 +312,12 @@ static void attn_heads(void* p, size_t lo, size_t hi) {
             }
         }
     }
-    free(sc);
 }
 
-void pyc_cpu_attention(const float* q, const float* k, const float* v, float* o, int B, int H, int S, int D,
-                       int causal, float scale) {
+int pyc_cpu_attention(const float* q, const float* k, const float* v, float* o, int B, int H, int S, int D,
+                      int causal, float scale) {
+    const size_t heads = (size_t)B * H;
+    const int nt = pyc_cpu_threads(heads);
     attn_ctx a;
     a.q = q;
     a.k = k;
@@ -325,7 +327,18 @@ void pyc_cpu_attention(const float* q, const float* k, const float* v, float* o,
     a.D = D;
     a.causal = causal;
     a.scale = scale;
-    parallel_for((size_t)B * H, attn_heads, &a);
+    if (heads == 0) {
+        return 0;
+    }
+    /* the ranges parallel_for cuts: ceil(heads / nt) heads each */
+    a.per = nt <= 1 ? heads : (heads + (size_t)nt - 1) / (size_t)nt;
+    a.rows = (float*)malloc((size_t)(nt > 1 ? nt : 1) * (size_t)S * sizeof(float));
+    if (!a.rows) {
+        return -1;
+    }
+    parallel_for(heads, attn_heads, &a);
+    free(a.rows);
+    return 0;
 }
 
 /* ---------------------------------------------------------------- fp8-weight GEMM */

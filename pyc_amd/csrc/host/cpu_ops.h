@@ -27,8 +27,9 @@ float pyc_op_eps(const char* name);
 
 void pyc_cpu_conv2d_nhwc(const float* x, const float* w, float* y, int N, int H, int W, int C, int K, int R, int S,
                          int ph, int pw, int sh, int sw);
-void pyc_cpu_attention(const float* q, const float* k, const float* v, float* o, int B, int H, int S, int D,
-                       int causal, float scale);
+/* 0, or -1 when its scratch rows cannot be allocated (o is then not written) */
+int pyc_cpu_attention(const float* q, const float* k, const float* v, float* o, int B, int H, int S, int D,
+                      int causal, float scale);
 void pyc_cpu_w8a16_gemm(const float* x, const uint8_t* wq, const float* scale, float* y, int M, int N, int K);
 void pyc_cpu_gelu(const float* x, float* y, size_t n);
 void pyc_cpu_layernorm(const float* x, const float* gamma, const float* beta, float* y, size_t rows, size_t D,

@@ -61,32 +61,53 @@ int pyc_hip_w8a16_reserve(int N, int K);
 /* chain kernel preconditions and its timeout word (gemm_w8a16.hip) */
 int pyc_hip_w8a16_chain_supported(int M, int nsteps, const int* N, const int* K);
 int pyc_hip_w8a16_chain_error_enqueue(int* host_dst, void* stream);
-/* 1 when a GEMM symbol takes alpha = 1, beta = 0 only (hip_kernels.c) */
+/* 1 when a GEMM symbol takes alpha = 1, beta = 0 only; 1 when it names the
+ * persistent kernel alone, which refuses beta != 0 and unaligned C or bias
+ * (hip_kernels.c) */
 int pyc_hip_gemm_symbol_unit_epilogue_only(const char* symbol);
+int pyc_hip_gemm_symbol_persistent_only(const char* symbol);
 
 static pyc_mutex g_dispatch_lock = PYC_MUTEX_INIT;
 
-/* Measured GEMM tile choice per (dtype, M, N, K), filled by
- * pyc_hip_autotune_gemm and read by build_plan; g_tune_gen is part of the
- * graph signature so a new choice recaptures. */
+/* Measured kernel choices, filled by pyc_hip_autotune_gemm (key: dtype, M,
+ * N, K) and pyc_hip_autotune_conv2d (key: dtype, N H W C K R S ph pw sh sw)
+ * and read by build_plan; g_tune_gen is part of the graph signature so a new
+ * choice recaptures. */
 typedef struct {
-    pyc_dtype dtype;
-    int m, n, k;
+    int key[12];
     char symbol[PYC_KERNEL_SYMBOL_MAX];
-} tuned_gemm;
+} tuned_entry;
 #define TUNED_MAX 32
-static tuned_gemm g_tuned[TUNED_MAX];
+static tuned_entry g_tuned[TUNED_MAX];
 static int g_tuned_count;
+static tuned_entry g_tuned_conv[TUNED_MAX];
+static int g_tuned_conv_count;
 static uint64_t g_tune_gen;
 
-static const char* tuned_symbol(pyc_dtype t, int m, int n, int k) {
+static const char* tuned_find(const tuned_entry* tab, int count, const int* key) {
     int i;
-    for (i = 0; i < g_tuned_count; ++i) {
-        if (g_tuned[i].dtype == t && g_tuned[i].m == m && g_tuned[i].n == n && g_tuned[i].k == k) {
-            return g_tuned[i].symbol;
+    for (i = 0; i < count; ++i) {
+        if (memcmp(tab[i].key, key, sizeof(tab[i].key)) == 0) {
+            return tab[i].symbol;
         }
     }
     return NULL;
+}
+
+static const char* tuned_symbol(pyc_dtype t, int m, int n, int k) {
+    int key[12] = {0};
+    key[0] = (int)t;
+    key[1] = m;
+    key[2] = n;
+    key[3] = k;
+    return tuned_find(g_tuned, g_tuned_count, key);
+}
+
+static const char* tuned_conv_symbol(pyc_dtype t, const int* conv11) {
+    int key[12] = {0};
+    key[0] = (int)t;
+    memcpy(&key[1], conv11, 11 * sizeof(int));
+    return tuned_find(g_tuned_conv, g_tuned_conv_count, key);
 }
 
 /* ---------------------------------------------------------------- env */
@@ -235,6 +256,8 @@ typedef struct {
     int attn[5];  /* B H S D causal */
     size_t elems; /* GELU: elements; LAYERNORM: rows (m) x last dim (n) */
     float eps;    /* LAYERNORM epsilon */
+    int chain_len; /* fp8 steps: >= 2 on the first step of a chain launch (its length), 0 on the chain's
+                    * other steps; 1 for every step that launches on its own */
     char symbol[PYC_KERNEL_SYMBOL_MAX];
 } hip_step;
 
@@ -274,31 +297,25 @@ static int value_private(const hip_plan* p, int v, size_t reader) {
 
 /* Number of consecutive fp8-weight steps from step s that run as one chain
  * launch (pyc_hip_w8a16_chain_dispatch): each reads the previous one's output,
- * which nothing else reads, and the chain so far meets the chain kernel's
- * preconditions (pyc_hip_w8a16_chain_supported: K % 128 == 0 and N % 64 == 0
- * for every step, unit and split-K slot limits). 1 when step s starts no
- * chain; those steps run one launch each on the per-layer kernel. */
+ * which nothing else reads, and every step meets the chain kernel's
+ * preconditions (pyc_hip_w8a16_chain_supported: K % 128 == 0 and N % 64 == 0,
+ * unit and split-K slot limits; they hold step by step, so each step is
+ * checked once, on its own). 1 when step s starts no chain; those steps run
+ * one launch each on the per-layer kernel. build_plan stores the result in
+ * each step's chain_len. */
 #define HIP_CHAIN_MAX_STEPS 32
 static size_t w8_chain_len(const hip_plan* p, size_t s) {
     size_t e = s;
-    int cn[HIP_CHAIN_MAX_STEPS], ck[HIP_CHAIN_MAX_STEPS];
     const hip_step* a = &p->steps[s];
-    if (a->kind != ST_W8A16 || a->add_mode != ADD_NONE) {
+    if (a->kind != ST_W8A16 || a->add_mode != ADD_NONE || !pyc_hip_w8a16_chain_supported(a->m, 1, &a->n, &a->k)) {
         return 1;
     }
-    cn[0] = a->n;
-    ck[0] = a->k;
     while (e + 1 < p->nsteps && e + 1 - s < HIP_CHAIN_MAX_STEPS) {
         const hip_step* cur = &p->steps[e];
         const hip_step* nx = &p->steps[e + 1];
-        const size_t len = e + 2 - s;
         if (nx->kind != ST_W8A16 || nx->add_mode != ADD_NONE || nx->in[0] != cur->out || nx->m != cur->m ||
-            nx->k != cur->n || !value_private(p, cur->out, e + 1)) {
-            break;
-        }
-        cn[len - 1] = nx->n;
-        ck[len - 1] = nx->k;
-        if (!pyc_hip_w8a16_chain_supported(a->m, (int)len, cn, ck)) {
+            nx->k != cur->n || !value_private(p, cur->out, e + 1) ||
+            !pyc_hip_w8a16_chain_supported(nx->m, 1, &nx->n, &nx->k)) {
             break;
         }
         ++e;
@@ -310,8 +327,7 @@ static size_t w8_chain_len(const hip_plan* p, size_t s) {
 static int plan_has_chain(const hip_plan* p) {
     size_t s;
     for (s = 0; s < p->nsteps; ++s) {
-        const size_t clen = w8_chain_len(p, s);
-        if (clen >= 2) {
+        if (p->steps[s].chain_len >= 2) {
             return 1;
         }
     }
@@ -388,6 +404,13 @@ static void absorb_epilogue(const pyc_ir_module* m, int prod, size_t rows, size_
         set_value(plan, next, &plan->vshape[prod], plan->vdtype[prod]);
         covered[next] = 1;
     }
+}
+
+/* The shape-chosen GEMM symbol of a dtype, which takes every shape, epilogue
+ * and alignment (the planned symbol when a tuned, promoted or env-selected one
+ * cannot run a step). */
+static const char* general_gemm_symbol(pyc_dtype t) {
+    return t == PYC_DTYPE_BF16 ? "hip_gemm_bf16_nn" : t == PYC_DTYPE_F16 ? "hip_gemm_f16_nn" : "hip_gemm_f32_nn_64x64";
 }
 
 static const char* default_gemm_symbol(pyc_dtype t) {
@@ -515,10 +538,12 @@ static int build_plan(const pyc_ir_module* m, hip_plan* plan) {
                     return 1; /* the fp8 epilogue is scale (+ReLU) only */
                 }
                 if (st->kind == ST_GEMM && st->add_mode == ADD_MATRIX &&
-                    pyc_hip_gemm_symbol_unit_epilogue_only(st->symbol)) {
-                    /* a matrix addend runs as beta = 1, which a tuned or
-                     * promoted unit-epilogue variant does not take */
-                    set_reason(st->symbol, sizeof(st->symbol), default_gemm_symbol(st->dtype));
+                    (pyc_hip_gemm_symbol_unit_epilogue_only(st->symbol) ||
+                     pyc_hip_gemm_symbol_persistent_only(st->symbol))) {
+                    /* a matrix addend runs as beta = 1, which a tuned,
+                     * promoted or env-selected unit-epilogue or
+                     * persistent-only variant does not take */
+                    set_reason(st->symbol, sizeof(st->symbol), general_gemm_symbol(st->dtype));
                 }
                 plan->nsteps++;
                 break;
@@ -574,6 +599,9 @@ static int build_plan(const pyc_ir_module* m, hip_plan* plan) {
                 }
                 set_reason(st->symbol, sizeof(st->symbol),
                            st->dtype == PYC_DTYPE_BF16 ? "hip_conv2d_bf16" : "hip_conv2d_f16");
+                if (tuned_conv_symbol(st->dtype, st->conv)) {
+                    set_reason(st->symbol, sizeof(st->symbol), tuned_conv_symbol(st->dtype, st->conv));
+                }
                 memset(&out_shape, 0, sizeof(out_shape));
                 out_shape.rank = 4;
                 out_shape.dims[0] = st->conv[0];
@@ -708,6 +736,15 @@ static int build_plan(const pyc_ir_module* m, hip_plan* plan) {
             default:
                 return 1; /* ADD/RELU not absorbed, CONST, REDUCE_SUM */
         }
+    }
+    for (i = 0; i < plan->nsteps;) {
+        const size_t clen = w8_chain_len(plan, i);
+        size_t j;
+        plan->steps[i].chain_len = (int)clen;
+        for (j = 1; j < clen; ++j) {
+            plan->steps[i + j].chain_len = 0;
+        }
+        i += clen;
     }
     return 0;
 }
@@ -982,7 +1019,7 @@ static int enqueue_steps(const pyc_ir_module* m, const hip_plan* plan, void* con
     for (s = 0; s < plan->nsteps; ++s) {
         const hip_step* st = &plan->steps[s];
         void* out = vp[st->out];
-        const size_t clen = w8_chain_len(plan, s);
+        const size_t clen = (size_t)st->chain_len;
         if (clen >= 2) {
             /* the whole run of fp8-weight steps in one launch */
             const void* wq[HIP_CHAIN_MAX_STEPS];
@@ -1030,6 +1067,12 @@ static int enqueue_steps(const pyc_ir_module* m, const hip_plan* plan, void* con
             case ST_GEMM:
                 rc = pyc_hip_gemm_dispatch(st->symbol, st->m, st->n, st->k, vp[st->in[0]],
                                            vp[st->in[1]], out, 1.0f, beta, bias, epi, st_stream);
+                if (rc == -1 && pyc_hip_gemm_symbol_persistent_only(st->symbol)) {
+                    /* the persistent kernel refused this call's alignment (a
+                     * caller's C or bias tensor off a 16-byte boundary) */
+                    rc = pyc_hip_gemm_dispatch(general_gemm_symbol(st->dtype), st->m, st->n, st->k, vp[st->in[0]],
+                                               vp[st->in[1]], out, 1.0f, beta, bias, epi, st_stream);
+                }
                 break;
             case ST_W8A16:
                 rc = pyc_hip_w8a16_gemm_dispatch(st->symbol, st->m, st->n, st->k, vp[st->in[0]],
@@ -1281,9 +1324,8 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
     sig = fnv(sig, &g_tune_gen, sizeof(g_tune_gen));
     /* the planned kernels: an env or registry change of a symbol recaptures */
     for (i = 0; i < plan.nsteps; ++i) {
-        const size_t clen = w8_chain_len(&plan, i);
         sig = fnv(sig, plan.steps[i].symbol, strlen(plan.steps[i].symbol));
-        sig = fnv(sig, &clen, sizeof(clen));
+        sig = fnv(sig, &plan.steps[i].chain_len, sizeof(int));
     }
     for (i = 0; i < m->op_count; ++i) {
         if (plan.input_ordinal[i] >= 0) {
@@ -1328,7 +1370,7 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
         if (use_graph) {
             /* the fp8 GEMM's split-K workspace cannot be allocated inside a capture */
             for (i = 0; i < plan.nsteps; ++i) {
-                const size_t clen = w8_chain_len(&plan, i);
+                const size_t clen = (size_t)plan.steps[i].chain_len;
                 if (clen >= 2) {
                     int cn[HIP_CHAIN_MAX_STEPS], ck[HIP_CHAIN_MAX_STEPS];
                     size_t c;
@@ -1473,7 +1515,7 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
         const char* sym = NULL;
         for (i = 0; i < plan.nsteps; ++i) {
             if (plan.steps[i].kind == ST_GEMM || plan.steps[i].kind == ST_W8A16) {
-                sym = w8_chain_len(&plan, i) >= 2 ? "hip_w8a16_chain_e4m3" : plan.steps[i].symbol;
+                sym = plan.steps[i].chain_len >= 2 ? "hip_w8a16_chain_e4m3" : plan.steps[i].symbol;
                 break;
             }
         }
@@ -1777,10 +1819,11 @@ pyc_cuda_dispatch_status pyc_cuda_dispatch(const pyc_ir_module* module, const py
  * symbol for that shape. Returns the number of timed variants (symbols and
  * mean ms in syms/ms), 0 when nothing could be timed, -1 on bad arguments. */
 /* Fills `bytes` of device memory with uniform values in [-1, 1) of `dtype`
- * (xorshift64), a 1 MiB host pattern repeated: timing on real-looking data,
+ * (xorshift64; [0, 1) with nonneg, as activations after a ReLU), a 1 MiB
+ * host pattern repeated: timing on real-looking data,
  * since constant operands switch less logic, draw less power and let the
  * clock run higher than a model's data does. */
-static int fill_operand(void* dst, size_t bytes, pyc_dtype dtype, uint64_t seed) {
+static int fill_operand(void* dst, size_t bytes, pyc_dtype dtype, uint64_t seed, int nonneg) {
     const size_t chunk = (size_t)1 << 20;
     uint8_t* pat = (uint8_t*)malloc(chunk);
     uint64_t x = seed * 0x9E3779B97F4A7C15ull + 1;
@@ -1794,7 +1837,10 @@ static int fill_operand(void* dst, size_t bytes, pyc_dtype dtype, uint64_t seed)
         x ^= x << 13;
         x ^= x >> 7;
         x ^= x << 17;
-        f = (float)((double)(x >> 40) / (double)(1ull << 24)) * 2.0f - 1.0f;
+        f = (float)((double)(x >> 40) / (double)(1ull << 24));
+        if (!nonneg) {
+            f = f * 2.0f - 1.0f;
+        }
         if (dtype == PYC_DTYPE_F32) {
             memcpy(pat + 4 * i, &f, 4);
         } else {
@@ -1827,70 +1873,38 @@ static int cmp_double(const void* a, const void* b) {
     return x < y ? -1 : x > y;
 }
 
-int pyc_hip_autotune_gemm(pyc_dtype dtype, int M, int N, int K, int iters, char* syms, size_t sym_stride,
-                          double* ms, int cap) {
-    /* one entry per distinct kernel: the reference's fp32 alias
-     * ada_gemm_k64_warp32_async_f32 runs hip_gemm_f32_nn_64x64's kernel with a
-     * narrower epilogue, so timing it would only pick between equal launches */
-    static const char* const cands[] = {"hip_gemm_bf16_nn_256x256_lds", "hip_gemm_bf16_nn_256x256",
-                                        "hip_gemm_bf16_nn_128x128", "hip_gemm_bf16_nn", "cutlass_gemm_tensorcore_bf16",
-                                        "hip_gemm_f16_nn_256x256_lds", "hip_gemm_f16_nn", "hip_gemm_f32_nn_64x64"};
-    enum { NCAND = sizeof(cands) / sizeof(cands[0]), ROUNDS = 3 };
-    const size_t eb = dtype_bytes(dtype);
-    void *a = NULL, *b = NULL, *c = NULL;
-    hipStream_t s = NULL;
-    hipEvent_t e0 = NULL, e1 = NULL;
-    int devices = 0;
-    char best[PYC_KERNEL_SYMBOL_MAX] = "";
-    double best_ms = 0.0;
-    double t_round[NCAND][ROUNDS];
-    int live[NCAND];
-    int n = 0, r;
-    size_t i;
-    if ((dtype != PYC_DTYPE_F32 && dtype != PYC_DTYPE_BF16 && dtype != PYC_DTYPE_F16) || M <= 0 || N <= 0 ||
-        K <= 0 || iters <= 0 || !syms || sym_stride == 0 || !ms || cap <= 0) {
-        return -1;
+/* Times candidate launches for the autotune entry points: each live
+ * candidate once (which also loads its code), a settle phase on the first live
+ * one (the clock of an idle card ramps over the first tens of milliseconds of
+ * load: 50 ms, at most 2000 launches), then ROUNDS interleaved rounds of
+ * `iters` launches per candidate, each candidate's time its median round, so
+ * a clock or power drift during tuning spreads over all candidates instead of
+ * favouring one. launch(i) enqueues candidate i on s and returns 0. On return
+ * live[i] says whether candidate i was timed and ms[i] is its median ms. */
+#define TUNE_ROUNDS 3
+static void time_candidates(int ncand, int (*launch)(int i, void* ctx, hipStream_t s), void* ctx, hipStream_t s,
+                            hipEvent_t e0, hipEvent_t e1, int iters, int* live, double* ms) {
+    double t_round[32][TUNE_ROUNDS];
+    int i, r, first = -1;
+    for (i = 0; i < ncand && i < 32; ++i) {
+        live[i] = live[i] && launch(i, ctx, s) == 0;
+        if (live[i] && first < 0) {
+            first = i;
+        }
     }
-    if (env_true("PYC_CUDA_DISABLE") || hipGetDeviceCount(&devices) != hipSuccess || devices <= 0) {
-        (void)hipGetLastError();
-        return 0;
-    }
-    pyc_mutex_lock(&g_dispatch_lock);
-    if (hipMalloc(&a, (size_t)M * K * eb) != hipSuccess || hipMalloc(&b, (size_t)K * N * eb) != hipSuccess ||
-        hipMalloc(&c, (size_t)M * N * eb) != hipSuccess || hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess ||
-        hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess ||
-        fill_operand(a, (size_t)M * K * eb, dtype, 1) != 0 || fill_operand(b, (size_t)K * N * eb, dtype, 2) != 0) {
-        goto done;
-    }
-    /* candidates of this dtype whose preconditions the shape meets (one
-     * launch each, which also loads their code) */
-    for (i = 0; i < NCAND; ++i) {
-        const int want = dtype == PYC_DTYPE_BF16 ? strstr(cands[i], "bf16") != NULL
-                         : dtype == PYC_DTYPE_F16 ? strstr(cands[i], "f16") != NULL && !strstr(cands[i], "bf16")
-                                                  : strstr(cands[i], "f32") != NULL;
-        live[i] = want && pyc_hip_gemm_dispatch(cands[i], M, N, K, a, b, c, 1.0f, 0.0f, NULL, 0, s) == 0;
-    }
-    /* settle: the clock of an idle card ramps over the first tens of
-     * milliseconds of load; the first live candidate runs for 50 ms (at most
-     * 2000 launches) before anything is timed */
-    for (i = 0; i < NCAND && !live[i]; ++i) {
-    }
-    if (i < NCAND) {
+    if (first >= 0) {
         const double t_end = now_ms() + 50.0;
         int launches = 0;
         while (now_ms() < t_end && launches < 2000) {
             int j;
             for (j = 0; j < 4; ++j, ++launches) {
-                (void)pyc_hip_gemm_dispatch(cands[i], M, N, K, a, b, c, 1.0f, 0.0f, NULL, 0, s);
+                (void)launch(first, ctx, s);
             }
             (void)hipStreamSynchronize(s);
         }
     }
-    /* ROUNDS interleaved rounds of `iters` launches per candidate; each
-     * candidate's time is its median round, so a clock or power drift during
-     * tuning spreads over all candidates instead of favouring one */
-    for (r = 0; r < ROUNDS; ++r) {
-        for (i = 0; i < NCAND; ++i) {
+    for (r = 0; r < TUNE_ROUNDS; ++r) {
+        for (i = 0; i < ncand && i < 32; ++i) {
             float t = 0.0f;
             int it, ok;
             if (!live[i]) {
@@ -1898,7 +1912,7 @@ int pyc_hip_autotune_gemm(pyc_dtype dtype, int M, int N, int K, int iters, char*
             }
             ok = hipEventRecord(e0, s) == hipSuccess;
             for (it = 0; ok && it < iters; ++it) {
-                ok = pyc_hip_gemm_dispatch(cands[i], M, N, K, a, b, c, 1.0f, 0.0f, NULL, 0, s) == 0;
+                ok = launch(i, ctx, s) == 0;
             }
             ok = ok && hipEventRecord(e1, s) == hipSuccess && hipEventSynchronize(e1) == hipSuccess &&
                  hipEventElapsedTime(&t, e0, e1) == hipSuccess;
@@ -1909,38 +1923,119 @@ int pyc_hip_autotune_gemm(pyc_dtype dtype, int M, int N, int K, int iters, char*
             t_round[i][r] = (double)t / iters;
         }
     }
-    for (i = 0; i < NCAND && n < cap; ++i) {
+    for (i = 0; i < ncand && i < 32; ++i) {
+        if (live[i]) {
+            qsort(t_round[i], TUNE_ROUNDS, sizeof(double), cmp_double);
+            ms[i] = t_round[i][TUNE_ROUNDS / 2];
+        }
+    }
+}
+
+/* Records (key -> best) in a tuned table, replacing the key's entry or, when
+ * the table is full, its last slot. */
+static void tuned_store(tuned_entry* tab, int* count, int cap, const tuned_entry* e) {
+    int slot = *count, j;
+    for (j = 0; j < *count; ++j) {
+        if (memcmp(tab[j].key, e->key, sizeof(e->key)) == 0) {
+            slot = j;
+        }
+    }
+    if (slot == cap) {
+        slot = cap - 1;
+    } else if (slot == *count) {
+        (*count)++;
+    }
+    tab[slot] = *e;
+    g_tune_gen++;
+}
+
+typedef struct {
+    const char* const* cands;
+    int M, N, K;
+    void *a, *b, *c;
+} gemm_tune_ctx;
+
+static int gemm_tune_launch(int i, void* ctx, hipStream_t s) {
+    const gemm_tune_ctx* g = (const gemm_tune_ctx*)ctx;
+    return pyc_hip_gemm_dispatch(g->cands[i], g->M, g->N, g->K, g->a, g->b, g->c, 1.0f, 0.0f, NULL, 0, s);
+}
+
+/* Writes the timed candidates (symbol, median ms) to syms/ms and returns the
+ * index of the fastest in cands, or -1. */
+static int tune_report(const char* const* cands, int ncand, const int* live, const double* t, char* syms,
+                       size_t sym_stride, double* ms, int cap, int* n) {
+    int i, best = -1;
+    *n = 0;
+    for (i = 0; i < ncand && *n < cap; ++i) {
         if (!live[i]) {
             continue;
         }
-        qsort(t_round[i], ROUNDS, sizeof(double), cmp_double);
-        set_reason(syms + (size_t)n * sym_stride, sym_stride, cands[i]);
-        ms[n] = t_round[i][ROUNDS / 2];
-        if (best[0] == '\0' || ms[n] < best_ms) {
-            best_ms = ms[n];
-            set_reason(best, sizeof(best), cands[i]);
+        set_reason(syms + (size_t)(*n) * sym_stride, sym_stride, cands[i]);
+        ms[*n] = t[i];
+        if (best < 0 || t[i] < t[best]) {
+            best = i;
         }
-        ++n;
+        ++(*n);
     }
-    if (best[0] != '\0') {
-        int slot = g_tuned_count;
-        int j;
-        for (j = 0; j < g_tuned_count; ++j) {
-            if (g_tuned[j].dtype == dtype && g_tuned[j].m == M && g_tuned[j].n == N && g_tuned[j].k == K) {
-                slot = j;
-            }
-        }
-        if (slot == TUNED_MAX) {
-            slot = TUNED_MAX - 1; /* table full: the newest shape replaces the last slot */
-        } else if (slot == g_tuned_count) {
-            g_tuned_count++;
-        }
-        g_tuned[slot].dtype = dtype;
-        g_tuned[slot].m = M;
-        g_tuned[slot].n = N;
-        g_tuned[slot].k = K;
-        set_reason(g_tuned[slot].symbol, sizeof(g_tuned[slot].symbol), best);
-        g_tune_gen++;
+    return best;
+}
+
+int pyc_hip_autotune_gemm(pyc_dtype dtype, int M, int N, int K, int iters, char* syms, size_t sym_stride,
+                          double* ms, int cap) {
+    /* one entry per distinct kernel: the reference's fp32 alias
+     * ada_gemm_k64_warp32_async_f32 runs hip_gemm_f32_nn_64x64's kernel with a
+     * narrower epilogue, so timing it would only pick between equal launches */
+    static const char* const cands[] = {"hip_gemm_bf16_nn_256x256_lds", "hip_gemm_bf16_nn_256x256",
+                                        "hip_gemm_bf16_nn_128x128", "hip_gemm_bf16_nn", "cutlass_gemm_tensorcore_bf16",
+                                        "hip_gemm_f16_nn_256x256_lds", "hip_gemm_f16_nn", "hip_gemm_f32_nn_64x64"};
+    enum { NCAND = sizeof(cands) / sizeof(cands[0]) };
+    const size_t eb = dtype_bytes(dtype);
+    gemm_tune_ctx g;
+    hipStream_t s = NULL;
+    hipEvent_t e0 = NULL, e1 = NULL;
+    int devices = 0;
+    double t[NCAND];
+    int live[NCAND];
+    int n = 0, best;
+    size_t i;
+    if ((dtype != PYC_DTYPE_F32 && dtype != PYC_DTYPE_BF16 && dtype != PYC_DTYPE_F16) || M <= 0 || N <= 0 ||
+        K <= 0 || iters <= 0 || !syms || sym_stride == 0 || !ms || cap <= 0) {
+        return -1;
+    }
+    if (env_true("PYC_CUDA_DISABLE") || hipGetDeviceCount(&devices) != hipSuccess || devices <= 0) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    memset(&g, 0, sizeof(g));
+    g.cands = cands;
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    pyc_mutex_lock(&g_dispatch_lock);
+    if (hipMalloc(&g.a, (size_t)M * K * eb) != hipSuccess || hipMalloc(&g.b, (size_t)K * N * eb) != hipSuccess ||
+        hipMalloc(&g.c, (size_t)M * N * eb) != hipSuccess || hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess ||
+        fill_operand(g.a, (size_t)M * K * eb, dtype, 1, 0) != 0 || fill_operand(g.b, (size_t)K * N * eb, dtype, 2, 0) != 0) {
+        goto done;
+    }
+    /* candidates of this dtype (whether the shape meets their preconditions
+     * shows in their first launch) */
+    for (i = 0; i < NCAND; ++i) {
+        live[i] = dtype == PYC_DTYPE_BF16 ? strstr(cands[i], "bf16") != NULL
+                  : dtype == PYC_DTYPE_F16 ? strstr(cands[i], "f16") != NULL && !strstr(cands[i], "bf16")
+                                           : strstr(cands[i], "f32") != NULL;
+    }
+    time_candidates(NCAND, gemm_tune_launch, &g, s, e0, e1, iters, live, t);
+    best = tune_report(cands, NCAND, live, t, syms, sym_stride, ms, cap, &n);
+    if (best >= 0) {
+        tuned_entry e;
+        memset(&e, 0, sizeof(e));
+        e.key[0] = (int)dtype;
+        e.key[1] = M;
+        e.key[2] = N;
+        e.key[3] = K;
+        set_reason(e.symbol, sizeof(e.symbol), cands[best]);
+        tuned_store(g_tuned, &g_tuned_count, TUNED_MAX, &e);
     }
 done:
     if (s) {
@@ -1949,9 +2044,94 @@ done:
     if (e0) (void)hipEventDestroy(e0);
     if (e1) (void)hipEventDestroy(e1);
     if (s) (void)hipStreamDestroy(s);
-    if (a) (void)hipFree(a);
-    if (b) (void)hipFree(b);
-    if (c) (void)hipFree(c);
+    if (g.a) (void)hipFree(g.a);
+    if (g.b) (void)hipFree(g.b);
+    if (g.c) (void)hipFree(g.c);
+    (void)hipGetLastError();
+    pyc_mutex_unlock(&g_dispatch_lock);
+    return n;
+}
+
+typedef struct {
+    const char* const* cands;
+    int cv[11]; /* N H W C K R S ph pw sh sw */
+    void *x, *w, *y;
+    float* bias;
+} conv_tune_ctx;
+
+static int conv_tune_launch(int i, void* ctx, hipStream_t s) {
+    const conv_tune_ctx* g = (const conv_tune_ctx*)ctx;
+    const int* c = g->cv;
+    return pyc_hip_conv2d_dispatch(g->cands[i], c[0], c[1], c[2], c[3], c[4], c[5], c[6], c[7], c[8], c[9], c[10],
+                                   g->x, g->w, g->bias, 1, g->y, s);
+}
+
+int pyc_hip_autotune_conv2d(pyc_dtype dtype, int N, int H, int W, int C_in, int K, int R, int S, int pad_h,
+                            int pad_w, int stride_h, int stride_w, int iters, char* syms, size_t sym_stride,
+                            double* ms, int cap) {
+    /* the distinct paths (the reference's names are aliases of the first) */
+    static const char* const cands[] = {"hip_conv2d_bf16", "hip_conv2d_bf16_persist", "hip_conv2d_bf16_tiled",
+                                        "hip_conv2d_f16", "hip_conv2d_f16_persist", "hip_conv2d_f16_tiled"};
+    enum { NCAND = sizeof(cands) / sizeof(cands[0]) };
+    conv_tune_ctx g;
+    hipStream_t s = NULL;
+    hipEvent_t e0 = NULL, e1 = NULL;
+    int devices = 0;
+    double t[NCAND];
+    int live[NCAND];
+    int n = 0, best;
+    size_t i, xb, wb, yb;
+    int64_t P, Q;
+    if ((dtype != PYC_DTYPE_BF16 && dtype != PYC_DTYPE_F16) || N <= 0 || H <= 0 || W <= 0 || C_in <= 0 || K <= 0 ||
+        R <= 0 || S <= 0 || pad_h < 0 || pad_w < 0 || stride_h <= 0 || stride_w <= 0 || H + 2 * pad_h < R ||
+        W + 2 * pad_w < S || iters <= 0 || !syms || sym_stride == 0 || !ms || cap <= 0) {
+        return -1;
+    }
+    if (env_true("PYC_CUDA_DISABLE") || hipGetDeviceCount(&devices) != hipSuccess || devices <= 0) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    P = (H + 2 * pad_h - R) / stride_h + 1;
+    Q = (W + 2 * pad_w - S) / stride_w + 1;
+    xb = (size_t)N * H * W * C_in * 2;
+    wb = (size_t)K * R * S * C_in * 2;
+    yb = (size_t)N * (size_t)P * (size_t)Q * K * 2;
+    memset(&g, 0, sizeof(g));
+    g.cands = cands;
+    g.cv[0] = N; g.cv[1] = H; g.cv[2] = W; g.cv[3] = C_in; g.cv[4] = K; g.cv[5] = R; g.cv[6] = S;
+    g.cv[7] = pad_h; g.cv[8] = pad_w; g.cv[9] = stride_h; g.cv[10] = stride_w;
+    pyc_mutex_lock(&g_dispatch_lock);
+    if (hipMalloc(&g.x, xb) != hipSuccess || hipMalloc(&g.w, wb) != hipSuccess || hipMalloc(&g.y, yb) != hipSuccess ||
+        hipMalloc((void**)&g.bias, (size_t)K * sizeof(float)) != hipSuccess ||
+        hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess || hipEventCreate(&e0) != hipSuccess ||
+        hipEventCreate(&e1) != hipSuccess || fill_operand(g.x, xb, dtype, 1, 1) != 0 ||
+        fill_operand(g.w, wb, dtype, 2, 0) != 0 || fill_operand(g.bias, (size_t)K * sizeof(float), PYC_DTYPE_F32, 3, 0) != 0) {
+        goto done;
+    }
+    for (i = 0; i < NCAND; ++i) {
+        live[i] = (strstr(cands[i], "bf16") != NULL) == (dtype == PYC_DTYPE_BF16);
+    }
+    time_candidates(NCAND, conv_tune_launch, &g, s, e0, e1, iters, live, t);
+    best = tune_report(cands, NCAND, live, t, syms, sym_stride, ms, cap, &n);
+    if (best >= 0) {
+        tuned_entry e;
+        memset(&e, 0, sizeof(e));
+        e.key[0] = (int)dtype;
+        memcpy(&e.key[1], g.cv, sizeof(g.cv));
+        set_reason(e.symbol, sizeof(e.symbol), cands[best]);
+        tuned_store(g_tuned_conv, &g_tuned_conv_count, TUNED_MAX, &e);
+    }
+done:
+    if (s) {
+        (void)hipStreamSynchronize(s);
+    }
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (s) (void)hipStreamDestroy(s);
+    if (g.x) (void)hipFree(g.x);
+    if (g.w) (void)hipFree(g.w);
+    if (g.y) (void)hipFree(g.y);
+    if (g.bias) (void)hipFree(g.bias);
     (void)hipGetLastError();
     pyc_mutex_unlock(&g_dispatch_lock);
     return n;

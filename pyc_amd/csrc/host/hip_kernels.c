@@ -19,6 +19,7 @@
 #include "pyc/hip_backend.h"
 #include "pyc/kernel_registry.h"
 #include "pyc_mutex.h"
+#include "../kernels/kernel_info.h"
 
 /* ---------------------------------------------------------------- launchers (.hip) */
 int pyc_hip_gemm_half_launch(int is_bf16, int b_trans, int tile, int M, int N, int K,
@@ -36,7 +37,7 @@ int pyc_hip_gemm_f32_launch(int b_trans, int M, int N, int K, const void* A, con
                             void* stream);
 int pyc_hip_attention_launch(int is_bf16, int B, int H, int S, int D, int causal, const void* Q,
                              const void* K, const void* V, void* O, float scale, void* stream);
-int pyc_hip_conv2d_launch(int is_bf16, int N, int H, int W, int C, int K, int R, int S, int ph,
+int pyc_hip_conv2d_launch(int is_bf16, int path, int N, int H, int W, int C, int K, int R, int S, int ph,
                           int pw, int sh, int sw, const void* x, const void* w, const float* bias,
                           int relu, void* y, void* stream);
 int pyc_hip_w8a16_launch(int M, int N, int K, const void* X, const void* Wq, const float* scale,
@@ -53,8 +54,10 @@ int pyc_hip_layernorm_launch(int dtype, int rows, int D, float eps, const void* 
 
 /* ---------------------------------------------------------------- variant table */
 
-enum { VK_GEMM = 1, VK_ATTN = 2, VK_CONV = 3, VK_W8 = 4, VK_ELT = 5 };
+enum { VK_GEMM = 1, VK_ATTN = 2, VK_CONV = 3, VK_W8 = 4, VK_ELT = 5, VK_CHAIN = 6 };
 enum { VT_BF16 = 1, VT_F16 = 2, VT_F32 = 3 };
+/* conv2d paths (hip_variant.tile of a VK_CONV entry) */
+enum { CONV_AUTO = 0, CONV_PERSIST = -1, CONV_TILED = 1 };
 
 typedef struct {
     const char* op_key;
@@ -62,67 +65,109 @@ typedef struct {
     int kind;
     int dtype;
     int b_trans;  /* GEMM: B stored [N,K] */
-    int tile;     /* GEMM half tile edge; 0 = choose by shape; -1 = the persistent LDS-DMA kernel (4 waves, 256 x 256) */
+    int tile;     /* GEMM half tile edge; 0 = choose by shape; -1 = the persistent LDS-DMA kernel (4 waves,
+                   * 256 x 256). conv2d: CONV_AUTO / CONV_PERSIST / CONV_TILED */
     int unit_epilogue_only; /* alpha must be 1 and beta 0 */
     int priority;
-    double occupancy;      /* waves per SIMD / 8 for the variant's launch bounds */
-    size_t lds_bytes;
     int reg_class;
     pyc_kernel_workload_family workload;
 } hip_variant;
 
+/* LDS and occupancy are not in this table: each entry's registry descriptor
+ * takes them from the kernel it launches (kernel_info.h, variant_kinfo). */
 static const hip_variant k_variants[] = {
     /* bf16 MFMA GEMM tiles */
-    {"matmul", "hip_gemm_bf16_nt_256x256_lds", VK_GEMM, VT_BF16, 1, -1, 0, 125, 0.25, 131072, 2, PYC_KERNEL_WORKLOAD_LARGE_SQUARE},
-    {"matmul", "hip_gemm_bf16_nt_256x256", VK_GEMM, VT_BF16, 1, 256, 0, 120, 0.125, 131072, 3, PYC_KERNEL_WORKLOAD_LARGE_SQUARE},
-    {"matmul", "hip_gemm_bf16_nt_128x128", VK_GEMM, VT_BF16, 1, 128, 0, 110, 0.25, 65536, 2, PYC_KERNEL_WORKLOAD_SQUARE},
-    {"matmul", "hip_gemm_bf16_nn_256x256_lds", VK_GEMM, VT_BF16, 0, -1, 0, 118, 0.25, 163840, 2, PYC_KERNEL_WORKLOAD_LARGE_SQUARE},
-    {"matmul", "hip_gemm_bf16_nn_256x256", VK_GEMM, VT_BF16, 0, 256, 0, 115, 0.125, 131072, 3, PYC_KERNEL_WORKLOAD_LARGE_SQUARE},
-    {"matmul", "hip_gemm_bf16_nn_128x128", VK_GEMM, VT_BF16, 0, 128, 0, 105, 0.25, 65536, 2, PYC_KERNEL_WORKLOAD_SQUARE},
-    {"matmul", "hip_gemm_bf16_nt", VK_GEMM, VT_BF16, 1, 0, 0, 100, 0.125, 131072, 3, PYC_KERNEL_WORKLOAD_ANY},
-    {"matmul", "hip_gemm_bf16_nn", VK_GEMM, VT_BF16, 0, 0, 0, 100, 0.125, 131072, 3, PYC_KERNEL_WORKLOAD_ANY},
+    {"matmul", "hip_gemm_bf16_nt_256x256_lds", VK_GEMM, VT_BF16, 1, -1, 0, 125, 2, PYC_KERNEL_WORKLOAD_LARGE_SQUARE},
+    {"matmul", "hip_gemm_bf16_nt_256x256", VK_GEMM, VT_BF16, 1, 256, 0, 120, 3, PYC_KERNEL_WORKLOAD_LARGE_SQUARE},
+    {"matmul", "hip_gemm_bf16_nt_128x128", VK_GEMM, VT_BF16, 1, 128, 0, 110, 2, PYC_KERNEL_WORKLOAD_SQUARE},
+    {"matmul", "hip_gemm_bf16_nn_256x256_lds", VK_GEMM, VT_BF16, 0, -1, 0, 118, 2, PYC_KERNEL_WORKLOAD_LARGE_SQUARE},
+    {"matmul", "hip_gemm_bf16_nn_256x256", VK_GEMM, VT_BF16, 0, 256, 0, 115, 3, PYC_KERNEL_WORKLOAD_LARGE_SQUARE},
+    {"matmul", "hip_gemm_bf16_nn_128x128", VK_GEMM, VT_BF16, 0, 128, 0, 105, 2, PYC_KERNEL_WORKLOAD_SQUARE},
+    {"matmul", "hip_gemm_bf16_nt", VK_GEMM, VT_BF16, 1, 0, 0, 100, 3, PYC_KERNEL_WORKLOAD_ANY},
+    {"matmul", "hip_gemm_bf16_nn", VK_GEMM, VT_BF16, 0, 0, 0, 100, 3, PYC_KERNEL_WORKLOAD_ANY},
     /* fp16 MFMA GEMM */
-    {"matmul", "hip_gemm_f16_nt_256x256_lds", VK_GEMM, VT_F16, 1, -1, 0, 96, 0.25, 131072, 2, PYC_KERNEL_WORKLOAD_LARGE_SQUARE},
-    {"matmul", "hip_gemm_f16_nn_256x256_lds", VK_GEMM, VT_F16, 0, -1, 0, 96, 0.25, 163840, 2, PYC_KERNEL_WORKLOAD_LARGE_SQUARE},
-    {"matmul", "hip_gemm_f16_nt", VK_GEMM, VT_F16, 1, 0, 0, 95, 0.125, 131072, 3, PYC_KERNEL_WORKLOAD_ANY},
-    {"matmul", "hip_gemm_f16_nn", VK_GEMM, VT_F16, 0, 0, 0, 95, 0.125, 131072, 3, PYC_KERNEL_WORKLOAD_ANY},
+    {"matmul", "hip_gemm_f16_nt_256x256_lds", VK_GEMM, VT_F16, 1, -1, 0, 96, 2, PYC_KERNEL_WORKLOAD_LARGE_SQUARE},
+    {"matmul", "hip_gemm_f16_nn_256x256_lds", VK_GEMM, VT_F16, 0, -1, 0, 96, 2, PYC_KERNEL_WORKLOAD_LARGE_SQUARE},
+    {"matmul", "hip_gemm_f16_nt", VK_GEMM, VT_F16, 1, 0, 0, 95, 3, PYC_KERNEL_WORKLOAD_ANY},
+    {"matmul", "hip_gemm_f16_nn", VK_GEMM, VT_F16, 0, 0, 0, 95, 3, PYC_KERNEL_WORKLOAD_ANY},
     /* fp32 MFMA GEMM (true fp32) */
-    {"matmul", "hip_gemm_f32_nn_64x64", VK_GEMM, VT_F32, 0, 64, 0, 60, 0.25, 32768, 1, PYC_KERNEL_WORKLOAD_ANY},
-    {"matmul", "hip_gemm_f32_nt_64x64", VK_GEMM, VT_F32, 1, 64, 0, 55, 0.25, 32768, 1, PYC_KERNEL_WORKLOAD_ANY},
+    {"matmul", "hip_gemm_f32_nn_64x64", VK_GEMM, VT_F32, 0, 64, 0, 60, 1, PYC_KERNEL_WORKLOAD_ANY},
+    {"matmul", "hip_gemm_f32_nt_64x64", VK_GEMM, VT_F32, 1, 64, 0, 55, 1, PYC_KERNEL_WORKLOAD_ANY},
     /* reference symbol names (reference gemm/kernel.cu:105-145, ada_async_kernel.cu:252-266),
      * bound to the MI355X kernels with the reference's operand layouts */
-    {"matmul", "cutlass_gemm_tensorcore_f16", VK_GEMM, VT_F16, 1, 0, 0, 100, 0.125, 131072, 2, PYC_KERNEL_WORKLOAD_ANY},
-    {"matmul", "cutlass_gemm_tensorcore_bf16", VK_GEMM, VT_BF16, 0, 0, 0, 90, 0.125, 131072, 2, PYC_KERNEL_WORKLOAD_ANY},
-    {"matmul", "cutlass_gemm_simt_f32", VK_GEMM, VT_F32, 1, 64, 0, 10, 0.25, 32768, 1, PYC_KERNEL_WORKLOAD_ANY},
-    {"matmul", "ada_gemm_k64_warp32_async_f32", VK_GEMM, VT_F32, 0, 64, 1, 20, 0.25, 32768, 1, PYC_KERNEL_WORKLOAD_ANY},
+    {"matmul", "cutlass_gemm_tensorcore_f16", VK_GEMM, VT_F16, 1, 0, 0, 100, 2, PYC_KERNEL_WORKLOAD_ANY},
+    {"matmul", "cutlass_gemm_tensorcore_bf16", VK_GEMM, VT_BF16, 0, 0, 0, 90, 2, PYC_KERNEL_WORKLOAD_ANY},
+    {"matmul", "cutlass_gemm_simt_f32", VK_GEMM, VT_F32, 1, 64, 0, 10, 1, PYC_KERNEL_WORKLOAD_ANY},
+    {"matmul", "ada_gemm_k64_warp32_async_f32", VK_GEMM, VT_F32, 0, 64, 1, 20, 1, PYC_KERNEL_WORKLOAD_ANY},
     /* attention (reference attention/kernel.cu:64-90 names) */
-    {"attention", "hip_attention_bf16", VK_ATTN, VT_BF16, 0, 0, 0, 110, 0.25, 49152, 3, PYC_KERNEL_WORKLOAD_ANY},
-    {"attention", "hip_attention_f16", VK_ATTN, VT_F16, 0, 0, 0, 105, 0.25, 49152, 3, PYC_KERNEL_WORKLOAD_ANY},
-    {"attention", "cutlass_attention_f16", VK_ATTN, VT_F16, 0, 0, 0, 100, 0.25, 49152, 3, PYC_KERNEL_WORKLOAD_ANY},
-    {"attention", "cutlass_attention_bf16", VK_ATTN, VT_BF16, 0, 0, 0, 90, 0.25, 49152, 3, PYC_KERNEL_WORKLOAD_ANY},
-    /* conv2d (reference conv2d/kernel.cu:48-75 names) */
-    {"conv2d", "hip_conv2d_bf16", VK_CONV, VT_BF16, 0, 0, 0, 110, 0.125, 131072, 3, PYC_KERNEL_WORKLOAD_ANY},
-    {"conv2d", "hip_conv2d_f16", VK_CONV, VT_F16, 0, 0, 0, 105, 0.125, 131072, 3, PYC_KERNEL_WORKLOAD_ANY},
-    {"conv2d", "cutlass_conv2d_fprop_f16", VK_CONV, VT_F16, 0, 0, 0, 100, 0.125, 131072, 2, PYC_KERNEL_WORKLOAD_ANY},
-    {"conv2d", "cutlass_conv2d_fprop_bf16", VK_CONV, VT_BF16, 0, 0, 0, 90, 0.125, 131072, 2, PYC_KERNEL_WORKLOAD_ANY},
-    /* weight-only fp8 decode GEMM (no reference counterpart) */
-    {"matmul_w8a16", "hip_gemm_w8a16_e4m3", VK_W8, VT_BF16, 1, 0, 0, 100, 0.5, 16384, 2, PYC_KERNEL_WORKLOAD_WIDE_SKINNY},
+    {"attention", "hip_attention_bf16", VK_ATTN, VT_BF16, 0, 0, 0, 110, 3, PYC_KERNEL_WORKLOAD_ANY},
+    {"attention", "hip_attention_f16", VK_ATTN, VT_F16, 0, 0, 0, 105, 3, PYC_KERNEL_WORKLOAD_ANY},
+    {"attention", "cutlass_attention_f16", VK_ATTN, VT_F16, 0, 0, 0, 100, 3, PYC_KERNEL_WORKLOAD_ANY},
+    {"attention", "cutlass_attention_bf16", VK_ATTN, VT_BF16, 0, 0, 0, 90, 3, PYC_KERNEL_WORKLOAD_ANY},
+    /* conv2d (reference conv2d/kernel.cu:48-75 names) and the MI355X paths */
+    {"conv2d", "hip_conv2d_bf16", VK_CONV, VT_BF16, 0, CONV_AUTO, 0, 110, 3, PYC_KERNEL_WORKLOAD_ANY},
+    {"conv2d", "hip_conv2d_bf16_persist", VK_CONV, VT_BF16, 0, CONV_PERSIST, 0, 108, 3, PYC_KERNEL_WORKLOAD_ANY},
+    {"conv2d", "hip_conv2d_bf16_tiled", VK_CONV, VT_BF16, 0, CONV_TILED, 0, 104, 3, PYC_KERNEL_WORKLOAD_ANY},
+    {"conv2d", "hip_conv2d_f16", VK_CONV, VT_F16, 0, CONV_AUTO, 0, 105, 3, PYC_KERNEL_WORKLOAD_ANY},
+    {"conv2d", "hip_conv2d_f16_persist", VK_CONV, VT_F16, 0, CONV_PERSIST, 0, 103, 3, PYC_KERNEL_WORKLOAD_ANY},
+    {"conv2d", "hip_conv2d_f16_tiled", VK_CONV, VT_F16, 0, CONV_TILED, 0, 99, 3, PYC_KERNEL_WORKLOAD_ANY},
+    {"conv2d", "cutlass_conv2d_fprop_f16", VK_CONV, VT_F16, 0, CONV_AUTO, 0, 100, 2, PYC_KERNEL_WORKLOAD_ANY},
+    {"conv2d", "cutlass_conv2d_fprop_bf16", VK_CONV, VT_BF16, 0, CONV_AUTO, 0, 90, 2, PYC_KERNEL_WORKLOAD_ANY},
+    /* weight-only fp8 decode GEMM and the whole-chain kernel (no reference counterpart) */
+    {"matmul_w8a16", "hip_gemm_w8a16_e4m3", VK_W8, VT_BF16, 1, 0, 0, 100, 2, PYC_KERNEL_WORKLOAD_WIDE_SKINNY},
+    {"matmul_w8a16_chain", "hip_w8a16_chain_e4m3", VK_CHAIN, VT_BF16, 1, 0, 0, 100, 2, PYC_KERNEL_WORKLOAD_WIDE_SKINNY},
     /* GELU / LayerNorm, the reference's graph-break ops (no reference kernel) */
-    {"gelu", "hip_gelu_f32", VK_ELT, VT_F32, 0, 0, 0, 100, 1.0, 0, 1, PYC_KERNEL_WORKLOAD_ANY},
-    {"gelu", "hip_gelu_bf16", VK_ELT, VT_BF16, 0, 0, 0, 100, 1.0, 0, 1, PYC_KERNEL_WORKLOAD_ANY},
-    {"gelu", "hip_gelu_f16", VK_ELT, VT_F16, 0, 0, 0, 100, 1.0, 0, 1, PYC_KERNEL_WORKLOAD_ANY},
-    {"layernorm", "hip_layernorm_f32", VK_ELT, VT_F32, 0, 0, 0, 100, 1.0, 0, 1, PYC_KERNEL_WORKLOAD_ANY},
-    {"layernorm", "hip_layernorm_bf16", VK_ELT, VT_BF16, 0, 0, 0, 100, 1.0, 0, 1, PYC_KERNEL_WORKLOAD_ANY},
-    {"layernorm", "hip_layernorm_f16", VK_ELT, VT_F16, 0, 0, 0, 100, 1.0, 0, 1, PYC_KERNEL_WORKLOAD_ANY},
+    {"gelu", "hip_gelu_f32", VK_ELT, VT_F32, 0, 0, 0, 100, 1, PYC_KERNEL_WORKLOAD_ANY},
+    {"gelu", "hip_gelu_bf16", VK_ELT, VT_BF16, 0, 0, 0, 100, 1, PYC_KERNEL_WORKLOAD_ANY},
+    {"gelu", "hip_gelu_f16", VK_ELT, VT_F16, 0, 0, 0, 100, 1, PYC_KERNEL_WORKLOAD_ANY},
+    {"layernorm", "hip_layernorm_f32", VK_ELT, VT_F32, 0, 0, 0, 100, 1, PYC_KERNEL_WORKLOAD_ANY},
+    {"layernorm", "hip_layernorm_bf16", VK_ELT, VT_BF16, 0, 0, 0, 100, 1, PYC_KERNEL_WORKLOAD_ANY},
+    {"layernorm", "hip_layernorm_f16", VK_ELT, VT_F16, 0, 0, 0, 100, 1, PYC_KERNEL_WORKLOAD_ANY},
 };
+
+#define N_VARIANTS (sizeof(k_variants) / sizeof(k_variants[0]))
+
+/* The kernel an entry launches at the large shapes its descriptor is for:
+ * the persistent LDS-DMA kernel for the shape-chosen and _lds half GEMMs,
+ * the named tile otherwise; the persistent conv for the automatic and
+ * persistent conv paths; the head-dim-128 attention; the K % 128 fp8 kernel;
+ * the chain kernel; the register-resident LayerNorm. */
+static int variant_kinfo(const hip_variant* v, pyc_hip_kinfo* ki) {
+    const int bf = v->dtype == VT_BF16;
+    memset(ki, 0, sizeof(*ki));
+    switch (v->kind) {
+        case VK_GEMM:
+            if (v->dtype == VT_F32) {
+                return pyc_hip_kinfo_f32(v->b_trans, ki);
+            }
+            if (v->tile <= 0) {
+                return pyc_hip_kinfo_nt_lds(v->b_trans ? PYC_KI_NT_PERSIST : PYC_KI_NN_PERSIST, bf, ki);
+            }
+            return pyc_hip_kinfo_half(v->tile, v->b_trans, bf, ki);
+        case VK_ATTN:
+            return pyc_hip_kinfo_attention(128, bf, ki);
+        case VK_CONV:
+            return v->tile == CONV_TILED ? pyc_hip_kinfo_conv_tiled(256, bf, ki)
+                                         : pyc_hip_kinfo_nt_lds(PYC_KI_CONV_PERSIST, bf, ki);
+        case VK_W8:
+            return pyc_hip_kinfo_w8a16(PYC_KI_W8_LDS, ki);
+        case VK_CHAIN:
+            return pyc_hip_kinfo_w8a16(PYC_KI_W8_CHAIN, ki);
+        case VK_ELT:
+            return pyc_hip_kinfo_eltwise(strcmp(v->op_key, "gelu") == 0 ? 0 : 1,
+                                         v->dtype == VT_F32 ? 0 : bf ? 1 : 2, ki);
+        default:
+            return -1;
+    }
+}
 
 static const hip_variant* find_variant(const char* symbol, int kind) {
     size_t i;
     if (!symbol) {
         return NULL;
     }
-    for (i = 0; i < sizeof(k_variants) / sizeof(k_variants[0]); ++i) {
-        if (k_variants[i].kind == kind && strcmp(k_variants[i].symbol, symbol) == 0) {
+    for (i = 0; i < N_VARIANTS; ++i) {
+        if ((kind == 0 || k_variants[i].kind == kind) && strcmp(k_variants[i].symbol, symbol) == 0) {
             return &k_variants[i];
         }
     }
@@ -136,13 +181,22 @@ int pyc_hip_gemm_symbol_unit_epilogue_only(const char* symbol) {
     return v && v->unit_epilogue_only ? 1 : 0;
 }
 
+/* 1 when the GEMM symbol names the persistent LDS-DMA kernel alone (the _lds
+ * variants): its launcher refuses beta != 0, a C or bias not 16-byte aligned
+ * and shapes that are not whole 256 x 256 tiles, and such a symbol then
+ * fails instead of taking another kernel. */
+int pyc_hip_gemm_symbol_persistent_only(const char* symbol) {
+    const hip_variant* v = find_variant(symbol, VK_GEMM);
+    return v && v->tile == -1 ? 1 : 0;
+}
+
 int pyc_hip_kernel_symbol_count(const char* op_key) {
     size_t i;
     int n = 0;
     if (!op_key) {
         return 0;
     }
-    for (i = 0; i < sizeof(k_variants) / sizeof(k_variants[0]); ++i) {
+    for (i = 0; i < N_VARIANTS; ++i) {
         n += strcmp(k_variants[i].op_key, op_key) == 0;
     }
     return n;
@@ -263,7 +317,7 @@ int pyc_hip_conv2d_dispatch(const char* symbol, int N, int H, int W, int C_in, i
     if (H + 2 * pad_h < R || W + 2 * pad_w < S) {
         return -1;
     }
-    return pyc_hip_conv2d_launch(v->dtype == VT_BF16, N, H, W, C_in, K, R, S, pad_h, pad_w, stride_h,
+    return pyc_hip_conv2d_launch(v->dtype == VT_BF16, v->tile, N, H, W, C_in, K, R, S, pad_h, pad_w, stride_h,
                                  stride_w, x, w, bias, relu ? 1 : 0, y, stream);
 }
 
@@ -288,7 +342,7 @@ int pyc_hip_w8a16_gemm_dispatch(const char* symbol, int M, int N, int K, const v
 int pyc_hip_w8a16_chain_dispatch(const char* symbol, int M, int nsteps, const void* X, const void* const* Wq,
                                  const float* const* scale, const int* N, const int* K, const int* relu,
                                  void* Y, void* stream) {
-    if (!symbol || strcmp(symbol, "hip_w8a16_chain_e4m3") != 0) return -1;
+    if (!find_variant(symbol, VK_CHAIN)) return -1;
     if (M <= 0 || M > 32 || nsteps <= 0 || !X || !Wq || !scale || !N || !K || !relu || !Y) return -1;
     const int rc = pyc_hip_w8a16_chain_launch(M, nsteps, X, Wq, scale, N, K, relu, Y, stream);
     return rc == -3 ? -1 : rc;
@@ -297,7 +351,7 @@ int pyc_hip_w8a16_chain_dispatch(const char* symbol, int M, int nsteps, const vo
 int pyc_hip_w8a16_chain_dispatch_noalloc(const char* symbol, int M, int nsteps, const void* X, const void* const* Wq,
                                          const float* const* scale, const int* N, const int* K, const int* relu,
                                          void* Y, void* stream) {
-    if (!symbol || strcmp(symbol, "hip_w8a16_chain_e4m3") != 0) return -1;
+    if (!find_variant(symbol, VK_CHAIN)) return -1;
     if (M <= 0 || M > 32 || nsteps <= 0 || !X || !Wq || !scale || !N || !K || !relu || !Y) return -1;
     return pyc_hip_w8a16_chain_launch_noalloc(M, nsteps, X, Wq, scale, N, K, relu, Y, stream);
 }
@@ -330,15 +384,19 @@ static pyc_mutex g_registry_init_lock = PYC_MUTEX_INIT;
 static int g_registry_initialized = 0;
 
 /* Registers every variant under PYC_BACKEND_CUDA (the GPU backend slot) with
- * its LDS footprint, MFMA eligibility and CDNA4 preference, then honours
- * PYC_PROMOTED_GEMM_SYMBOL (reference registry/init.cu:32-78). */
+ * the LDS and resident waves of the kernel it launches (shared_mem_bytes;
+ * estimated_occupancy = waves per SIMD / 8, the most a CU holds), MFMA
+ * eligibility and CDNA4 preference, then honours PYC_PROMOTED_GEMM_SYMBOL
+ * (reference registry/init.cu:32-78). Runs at library load, before any HIP
+ * call: the figures are the ones compiled into the kernel sources, which
+ * pyc_hip_kernel_resources_query compares with the loaded code object. */
 void pyc_cutlass_registry_init(void) {
     size_t i;
     pyc_mutex_lock(&g_registry_init_lock);
     if (!g_registry_initialized) {
         const char* promoted = getenv("PYC_PROMOTED_GEMM_SYMBOL");
         g_registry_initialized = 1;
-        for (i = 0; i < sizeof(k_variants) / sizeof(k_variants[0]); ++i) {
+        for (i = 0; i < N_VARIANTS; ++i) {
             const hip_variant* v = &k_variants[i];
             pyc_kernel_desc d;
             memset(&d, 0, sizeof(d));
@@ -346,9 +404,12 @@ void pyc_cutlass_registry_init(void) {
             strncpy(d.symbol, v->symbol, sizeof(d.symbol) - 1);
             d.backend = PYC_BACKEND_CUDA;
             d.priority = v->priority;
-            d.estimated_occupancy = v->occupancy;
+            pyc_hip_kinfo ki;
+            if (variant_kinfo(v, &ki) == 0) {
+                d.estimated_occupancy = (double)ki.waves_per_simd / 8.0;
+                d.shared_mem_bytes = ki.lds_bytes;
+            }
             d.tensor_core_eligible = v->kind != VK_ELT;  /* GELU/LayerNorm: VALU only */
-            d.shared_mem_bytes = v->lds_bytes;
             d.reg_pressure_class = v->reg_class;
             d.preferred_workload_family = v->workload;
             d.preferred_hardware_family = PYC_KERNEL_HARDWARE_CDNA4;
@@ -370,6 +431,35 @@ __attribute__((constructor)) static void pyc_hip_registry_autoinit(void) {
 int pyc_cutlass_kernel_count(const char* op_key) {
     pyc_kernel_desc descs[64];
     return (int)pyc_kernel_collect(op_key, PYC_BACKEND_CUDA, descs, 64);
+}
+
+int pyc_hip_kernel_resources_query(const char* symbol, pyc_hip_kernel_resources* out) {
+    const hip_variant* v = find_variant(symbol, 0);
+    pyc_hip_kinfo ki;
+    int count = 0;
+    if (!v || !out || variant_kinfo(v, &ki) != 0) {
+        return -1;
+    }
+    memset(out, 0, sizeof(*out));
+    strncpy(out->kernel, ki.name, sizeof(out->kernel) - 1);
+    out->lds_bytes = ki.lds_bytes;
+    out->threads = ki.threads;
+    out->waves_per_simd = ki.waves_per_simd;
+    if (hipGetDeviceCount(&count) == hipSuccess && count > 0) {
+        hipFuncAttributes a;
+        int blocks = 0;
+        if (hipFuncGetAttributes(&a, ki.fn) == hipSuccess &&
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, ki.fn, ki.threads, 0) == hipSuccess) {
+            out->device = 1;
+            out->attr_lds_bytes = a.sharedSizeBytes;
+            out->attr_regs = a.numRegs;
+            out->attr_scratch_bytes = a.localSizeBytes;
+            out->attr_max_threads = a.maxThreadsPerBlock;
+            out->attr_blocks_per_cu = blocks;
+        }
+    }
+    (void)hipGetLastError();
+    return 0;
 }
 
 /* ---------------------------------------------------------------- device info */

@@ -139,6 +139,9 @@ __device__ inline float other_half(float x, int xaddr) {
 // its first blocks load during the current part's last phases; the next
 // part's Q is loaded in its last V phase and waited for with the K/V of the
 // following M phase.
+// LDS of the kernel below for head dim d: the K/V ring and the output staging.
+constexpr size_t attn_lds_bytes(int d) { return (size_t)kAttnRing * 2 * kAttnBK * d * 2 + (size_t)(kAttnWaves / 2) * 32 * d * 2; }
+
 template <typename T, int D>
 __global__ void __launch_bounds__(kAttnWaves * kWave, 1)
 attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
@@ -158,6 +161,7 @@ attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
     // output staging of the F phase, one area per SIMD: waves w and w + 4
     // (the two groups) never run F at the same time
     __shared__ __attribute__((aligned(1024))) uint16_t ostage[kAttnWaves / 2][32 * D];
+    static_assert(sizeof(smem) + sizeof(ostage) == attn_lds_bytes(D), "registered LDS figure");
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -630,4 +634,22 @@ extern "C" int pyc_hip_attention_launch(int is_bf16, int B, int H, int S, int D,
         return -1;
     }
     return e == hipSuccess ? 0 : -2;
+}
+
+// Registry figures: one 8-wave workgroup per CU (the LDS ring; at d = 64 the
+// register budget leaves room for no second one either).
+extern "C" int pyc_hip_kinfo_attention(int d, int is_bf16, pyc_hip_kinfo* out) {
+    using namespace pyc;
+    if (!out || (d != 64 && d != 128)) return -1;
+    out->name = d == 128 ? "attn_fwd_kernel<128>" : "attn_fwd_kernel<64>";
+    out->lds_bytes = attn_lds_bytes(d);
+    out->threads = kAttnWaves * kWave;
+    out->waves_per_simd = 2;
+    if (d == 128)
+        out->fn = is_bf16 ? reinterpret_cast<const void*>(&attn_fwd_kernel<bf16_t, 128>)
+                          : reinterpret_cast<const void*>(&attn_fwd_kernel<f16_t, 128>);
+    else
+        out->fn = is_bf16 ? reinterpret_cast<const void*>(&attn_fwd_kernel<bf16_t, 64>)
+                          : reinterpret_cast<const void*>(&attn_fwd_kernel<f16_t, 64>);
+    return 0;
 }

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "kernel_info.h"
+
 namespace pyc {
 
 typedef __bf16 bf16_t;

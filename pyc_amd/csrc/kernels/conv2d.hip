@@ -38,20 +38,26 @@ static hipError_t launch_conv(int N, int H, int W, int C, int K, int R, int S, i
 
 }  // namespace pyc
 
-extern "C" int pyc_hip_conv2d_persist_launch(int is_bf16, int Nimg, int H, int W, int C, int Kout, int R, int S,
-                                             int ph, int pw, int sh, int sw, const void* x, const void* w,
+extern "C" int pyc_hip_conv2d_persist_launch(int is_bf16, int tail, int Nimg, int H, int W, int C, int Kout, int R,
+                                             int S, int ph, int pw, int sh, int sw, const void* x, const void* w,
                                              const float* bias, int relu, void* y, void* stream);
 
-extern "C" int pyc_hip_conv2d_launch(int is_bf16, int N, int H, int W, int C, int K, int R, int S, int ph,
+// path: 0 = by shape (whole 256 x 256 tiles on the persistent kernel, a
+// partial second round on its tail kernel), -1 = every tile on the persistent
+// kernel, 1 = the register-staged tiles below; the persistent paths take the
+// tiles below for shapes outside their preconditions.
+extern "C" int pyc_hip_conv2d_launch(int is_bf16, int path, int N, int H, int W, int C, int K, int R, int S, int ph,
                                      int pw, int sh, int sw, const void* x, const void* w,
                                      const float* bias, int relu, void* y, void* stream) {
     using namespace pyc;
-    // whole-tile shapes with C % 64 == 0 take the persistent direct-LDS
-    // implicit GEMM (gemm_nt_lds.hip); it answers 1 when the shape is outside
-    // its preconditions
-    const int rc = pyc_hip_conv2d_persist_launch(is_bf16, N, H, W, C, K, R, S, ph, pw, sh, sw, x, w, bias, relu, y,
-                                                 stream);
-    if (rc != 1) return rc;
+    if (path != 1) {
+        // whole-tile shapes with C % 64 == 0 take the persistent direct-LDS
+        // implicit GEMM (gemm_nt_lds.hip); it answers 1 when the shape is
+        // outside its preconditions
+        const int rc = pyc_hip_conv2d_persist_launch(is_bf16, path == 0, N, H, W, C, K, R, S, ph, pw, sh, sw, x, w,
+                                                     bias, relu, y, stream);
+        if (rc != 1) return rc;
+    }
     hipStream_t s = (hipStream_t)stream;
     const long P = (H + 2 * ph - R) / sh + 1;
     const long Q = (W + 2 * pw - S) / sw + 1;
@@ -67,4 +73,22 @@ extern "C" int pyc_hip_conv2d_launch(int is_bf16, int N, int H, int W, int C, in
                 : launch_conv<f16_t, 128, 128>(N, H, W, C, K, R, S, ph, pw, sh, sw, x, w, bias, relu, y, s);
     }
     return e == hipSuccess ? 0 : -2;
+}
+
+// Registry figures of the general conv tiles (bias + ReLU instance shape):
+// 256: one workgroup per CU (256 VGPRs + 256 AGPRs); 128: two (LDS).
+extern "C" int pyc_hip_kinfo_conv_tiled(int tile, int is_bf16, pyc_hip_kinfo* out) {
+    using namespace pyc;
+    if (!out || (tile != 128 && tile != 256)) return -1;
+    out->threads = 4 * kWave;
+    out->lds_bytes = gemm_tile_lds_bytes(tile, tile);
+    out->waves_per_simd = tile == 256 ? 1 : 2;
+    out->name = tile == 256 ? "gemm_mfma_kernel<256x256, conv>" : "gemm_mfma_kernel<128x128, conv>";
+    if (tile == 256)
+        out->fn = is_bf16 ? reinterpret_cast<const void*>(&gemm_mfma_kernel<bf16_t, 256, 256, 2, 2, true, true, true>)
+                          : reinterpret_cast<const void*>(&gemm_mfma_kernel<f16_t, 256, 256, 2, 2, true, true, true>);
+    else
+        out->fn = is_bf16 ? reinterpret_cast<const void*>(&gemm_mfma_kernel<bf16_t, 128, 128, 2, 2, true, true, true>)
+                          : reinterpret_cast<const void*>(&gemm_mfma_kernel<f16_t, 128, 128, 2, 2, true, true, true>);
+    return 0;
 }

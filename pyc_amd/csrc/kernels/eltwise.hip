@@ -353,3 +353,27 @@ extern "C" int pyc_hip_layernorm_launch(int dtype, int rows, int D, float eps, c
         default: return -1;
     }
 }
+
+// Registry figures: GELU (kid 0) and the register-resident LayerNorm at up
+// to 8 chunks per lane (kid 1), 256-thread workgroups, no LDS; dtype 0 fp32,
+// 1 bf16, 2 fp16. Waves per SIMD from each instance's register count.
+extern "C" int pyc_hip_kinfo_eltwise(int kid, int dtype, pyc_hip_kinfo* out) {
+    using namespace pyc;
+    if (!out || dtype < 0 || dtype > 2 || kid < 0 || kid > 1) return -1;
+    out->threads = 256;
+    out->lds_bytes = 0;
+    if (kid == 0) {
+        out->name = "gelu_kernel";
+        out->waves_per_simd = 8;
+        out->fn = dtype == 0 ? reinterpret_cast<const void*>(&gelu_kernel<float>)
+                  : dtype == 1 ? reinterpret_cast<const void*>(&gelu_kernel<bf16_t>)
+                               : reinterpret_cast<const void*>(&gelu_kernel<f16_t>);
+    } else {
+        out->name = "layernorm_reg_kernel<8>";
+        out->waves_per_simd = dtype == 0 ? 7 : dtype == 1 ? 3 : 4;
+        out->fn = dtype == 0 ? reinterpret_cast<const void*>(&layernorm_reg_kernel<float, 8>)
+                  : dtype == 1 ? reinterpret_cast<const void*>(&layernorm_reg_kernel<bf16_t, 8>)
+                               : reinterpret_cast<const void*>(&layernorm_reg_kernel<f16_t, 8>);
+    }
+    return 0;
+}

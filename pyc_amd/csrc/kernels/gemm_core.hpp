@@ -33,6 +33,9 @@ struct ConvGeom {
     int H, W, C, S, P, Q, pad_h, pad_w, stride_h, stride_w;
 };
 
+// LDS of a BM x BN tile of the kernel below: A and B, two k stages each.
+constexpr size_t gemm_tile_lds_bytes(int bm, int bn) { return (size_t)2 * (bm + bn) * kGemmBK * 2; }
+
 template <typename T, int BM, int BN, int WM, int WN, bool BT, bool GUARD, bool CONV>
 __global__ void __launch_bounds__(WM * WN * kWave, 1)
 gemm_mfma_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
@@ -53,6 +56,7 @@ gemm_mfma_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
 
     __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kGemmBK];
     __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN * kGemmBK];
+    static_assert(sizeof(As) + sizeof(Bs) == gemm_tile_lds_bytes(BM, BN), "registered LDS figure");
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;

@@ -202,6 +202,7 @@ gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ B, float*
 // lanes of each k slot read 16 consecutive n of rows 4 apart, which the
 // swizzle puts in four different 16-bank groups.
 constexpr int kF32Stages = 4;
+constexpr size_t kF32DmaLds = (size_t)kF32Stages * 2 * kF32BM * kF32BK * 4;
 
 template <bool BT>
 __global__ void __launch_bounds__(512, 1)
@@ -209,6 +210,7 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
                     int M, int N, int K, float alpha, float beta, const float* __restrict__ bias,
                     int epi, int group_m) {
     __shared__ __attribute__((aligned(1024))) float smem[kF32Stages * 2 * kF32BM * kF32BK];
+    static_assert(sizeof(smem) == kF32DmaLds, "registered LDS figure");
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -407,4 +409,18 @@ extern "C" int pyc_hip_gemm_f32_launch(int b_trans, int M, int N, int K, const v
         else hipLaunchKernelGGL((gemm_f32_kernel<false, true>), grid, block, 0, s, a, b, c, M, N, K, alpha, beta, bias, epi);
     }
     return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+// Registry figures of the LDS-DMA kernel: 128 KB of LDS, one 8-wave
+// workgroup per CU (two waves per SIMD).
+extern "C" int pyc_hip_kinfo_f32(int b_trans, pyc_hip_kinfo* out) {
+    using namespace pyc;
+    if (!out) return -1;
+    out->name = "gemm_f32_dma_kernel";
+    out->lds_bytes = kF32DmaLds;
+    out->threads = 512;
+    out->waves_per_simd = 2;
+    out->fn = b_trans ? reinterpret_cast<const void*>(&gemm_f32_dma_kernel<true>)
+                      : reinterpret_cast<const void*>(&gemm_f32_dma_kernel<false>);
+    return 0;
 }

@@ -25,6 +25,7 @@
 //    in groups of GROUP_M tile-rows, so concurrently running tiles on one XCD
 //    share A and B panels in that XCD's L2.
 #include "gemm_core.hpp"
+#include "kernel_info.h"
 
 namespace pyc {
 
@@ -80,4 +81,33 @@ extern "C" int pyc_hip_gemm_half_launch(int is_bf16, int b_trans, int tile, int 
     }
 #undef PYC_GEMM_CASE
     return e == hipSuccess ? 0 : -2;
+}
+
+// Registry figures of the tile instances above (whole-tile form; the guarded
+// form has the same LDS and launch bounds). Waves per SIMD: LDS and register
+// bound (256: 256 VGPRs + 256 AGPRs, one workgroup per CU; 128: two
+// workgroups; 64: five, by LDS).
+extern "C" int pyc_hip_kinfo_half(int tile, int b_trans, int is_bf16, pyc_hip_kinfo* out) {
+    using namespace pyc;
+    if (!out) return -1;
+    out->threads = 4 * kWave;
+#define PYC_KI(TL, W)                                                                                          \
+    do {                                                                                                       \
+        out->lds_bytes = gemm_tile_lds_bytes(TL, TL);                                                          \
+        out->waves_per_simd = W;                                                                               \
+        out->name = "gemm_mfma_kernel<" #TL "x" #TL ">";                                                       \
+        if (is_bf16)                                                                                           \
+            out->fn = b_trans ? reinterpret_cast<const void*>(&gemm_mfma_kernel<bf16_t, TL, TL, 2, 2, true, false, false>)   \
+                              : reinterpret_cast<const void*>(&gemm_mfma_kernel<bf16_t, TL, TL, 2, 2, false, false, false>); \
+        else                                                                                                   \
+            out->fn = b_trans ? reinterpret_cast<const void*>(&gemm_mfma_kernel<f16_t, TL, TL, 2, 2, true, false, false>)    \
+                              : reinterpret_cast<const void*>(&gemm_mfma_kernel<f16_t, TL, TL, 2, 2, false, false, false>);  \
+    } while (0)
+    switch (tile) {
+        case 256: PYC_KI(256, 1); return 0;
+        case 128: PYC_KI(128, 2); return 0;
+        case 64: PYC_KI(64, 5); return 0;
+        default: return -1;
+    }
+#undef PYC_KI
 }

@@ -29,11 +29,15 @@
 #include <type_traits>
 
 #include "common.hpp"
+#include "kernel_info.h"
 #include "lds_dma.hpp"
 
 namespace pyc {
 
 constexpr int kD_BM = 256, kD_BN = 256;
+// LDS of each kernel below (bytes), checked against its __shared__ array
+constexpr size_t kOneShotLds = 2 * (kD_BM + kD_BN) * 64 * 2;                 // two A+B stages
+constexpr size_t kPersistLds = (2 * (kD_BM + kD_BN) * 64 + 4 * 32 * 128) * 2;  // + C staging
 
 // LDS slot of logical 16-byte chunk `chunk` in a 128-byte stage row `row`.
 // A fragment read has 16 lanes on 16 consecutive rows at one logical chunk;
@@ -132,6 +136,7 @@ gemm_nt_lds4k64_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
     constexpr uint32_t STAGE_BYTES = kD_BM * BK * 2;  // 32 KB per operand
     // stages 0/1 of A, then of B; reused after the K loop to stage C
     __shared__ __attribute__((aligned(1024))) uint16_t smem[2 * (kD_BM + kD_BN) * BK];
+    static_assert(sizeof(smem) == kOneShotLds, "registered LDS figure");
     uint16_t* const As = smem;
     uint16_t* const Bs = smem + 2 * kD_BM * BK;
 
@@ -303,6 +308,7 @@ gemm_nt_persist_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
     constexpr int NSTORE = (128 / STAGE_ROWS) * (STAGE_ROWS / 4);  // 16-byte stores per lane per tile
     static_assert(2 * LOADS + NSTORE <= 48 && NSTORE == 32, "vmcnt accounting below assumes 16 loads per stage, 32 stores");
     __shared__ __attribute__((aligned(1024))) uint16_t smem[2 * (kD_BM + kD_BN) * BK + 4 * STAGE_ROWS * 128];
+    static_assert(sizeof(smem) == kPersistLds, "registered LDS figure");
     uint16_t* const As = smem;
     uint16_t* const Bs = smem + 2 * kD_BM * BK;
     uint16_t* const Cs = smem + 2 * (kD_BM + kD_BN) * BK;
@@ -625,6 +631,7 @@ gemm_nt_persist_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
 // gather the last pixel (never stored).
 constexpr int kTailBM = 160;
 constexpr int kTailStages = 3;
+constexpr size_t kTailLds = kTailStages * (kTailBM + kD_BN) * 64 * 2;
 
 template <typename T, int EPI>
 __global__ void __launch_bounds__(256, 1)
@@ -642,6 +649,7 @@ conv_tail_kernel(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt
     static_assert(kTailStages * STAGE_BYTES <= 160 * 1024, "LDS");
     static_assert(4 * (kTailBM / 2) * 128 * 2 <= kTailStages * STAGE_BYTES, "epilogue staging");
     __shared__ __attribute__((aligned(1024))) uint16_t smem[kTailStages * STAGE_BYTES / 2];
+    static_assert(sizeof(smem) == kTailLds, "registered LDS figure");
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -921,8 +929,9 @@ extern "C" int pyc_hip_gemm_nn_lds_launch(int is_bf16, int M, int N, int K, cons
 // when the shape is outside its preconditions (C % 64 == 0, N*P*Q and K_out
 // multiples of 256, x and w below 4 GiB, 16-byte aligned y and bias), 0 on
 // launch, -2 on a launch error.
-extern "C" int pyc_hip_conv2d_persist_launch(int is_bf16, int Nimg, int H, int W, int C, int Kout, int R, int S,
-                                             int ph, int pw, int sh, int sw, const void* x, const void* w,
+// tail = 0: every tile on the persistent kernel, whatever the round count.
+extern "C" int pyc_hip_conv2d_persist_launch(int is_bf16, int tail, int Nimg, int H, int W, int C, int Kout, int R,
+                                             int S, int ph, int pw, int sh, int sw, const void* x, const void* w,
                                              const float* bias, int relu, void* y, void* stream) {
     using namespace pyc;
     if (C % 64 != 0 || sh <= 0 || sw <= 0) return 1;
@@ -956,7 +965,7 @@ extern "C" int pyc_hip_conv2d_persist_launch(int is_bf16, int Nimg, int H, int W
     // the remaining pixels in 160-pixel tiles (conv_tail_kernel), when those
     // fit in one round as well.
     int m_full = (int)M, tail_tiles = 0;
-    if (tail_env && tiles_m * tiles_n > n_cu && tiles_m * tiles_n <= 2 * n_cu && n_cu / tiles_n > 0) {
+    if (tail && tail_env && tiles_m * tiles_n > n_cu && tiles_m * tiles_n <= 2 * n_cu && n_cu / tiles_n > 0) {
         const int m1 = (n_cu / tiles_n) * kD_BM;
         const int tm_tail = (int)((M - m1 + kTailBM - 1) / kTailBM);
         if (tm_tail * tiles_n <= n_cu) {
@@ -1007,4 +1016,43 @@ extern "C" int pyc_hip_conv2d_persist_launch(int is_bf16, int Nimg, int H, int W
 #undef PYC_TAIL
     }
     return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+// Registry figures of the kernels above (the epilogue-free instances; the
+// epilogue variants share their LDS and launch bounds). One 256-thread
+// workgroup per CU: the LDS, and 256 VGPRs + 256 AGPRs per lane.
+extern "C" int pyc_hip_kinfo_nt_lds(int kid, int is_bf16, pyc_hip_kinfo* out) {
+    using namespace pyc;
+    if (!out) return -1;
+    out->threads = 256;
+    out->waves_per_simd = 1;
+#define PYC_KI(NAME, LDS, F16, BF16) \
+    out->name = NAME;                \
+    out->lds_bytes = LDS;            \
+    out->fn = is_bf16 ? reinterpret_cast<const void*>(BF16) : reinterpret_cast<const void*>(F16)
+    switch (kid) {
+        case PYC_KI_NT_PERSIST:
+            PYC_KI("gemm_nt_persist_kernel", kPersistLds, (&gemm_nt_persist_kernel<f16_t, 24, 40, 0>),
+                   (&gemm_nt_persist_kernel<bf16_t, 24, 40, 0>));
+            return 0;
+        case PYC_KI_NN_PERSIST:
+            PYC_KI("gemm_nt_persist_kernel[B as k-rows]", kPersistLds,
+                   (&gemm_nt_persist_kernel<f16_t, 24, 40, 0, false, true>),
+                   (&gemm_nt_persist_kernel<bf16_t, 24, 40, 0, false, true>));
+            return 0;
+        case PYC_KI_NT_ONESHOT:
+            PYC_KI("gemm_nt_lds4k64_kernel", kOneShotLds, (&gemm_nt_lds4k64_kernel<f16_t, 24, 40>),
+                   (&gemm_nt_lds4k64_kernel<bf16_t, 24, 40>));
+            return 0;
+        case PYC_KI_CONV_PERSIST:
+            PYC_KI("gemm_nt_persist_kernel[conv]", kPersistLds, (&gemm_nt_persist_kernel<f16_t, 24, 40, 0, true>),
+                   (&gemm_nt_persist_kernel<bf16_t, 24, 40, 0, true>));
+            return 0;
+        case PYC_KI_CONV_TAIL:
+            PYC_KI("conv_tail_kernel", kTailLds, (&conv_tail_kernel<f16_t, 0>), (&conv_tail_kernel<bf16_t, 0>));
+            return 0;
+        default:
+            return -1;
+    }
+#undef PYC_KI
 }

@@ -51,6 +51,7 @@ gemm_small_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B
     constexpr int SEGS = BN / 16;                            // 32-byte segments per [K,N] k-row
     static_assert(STAGES >= 3, "ring");
     __shared__ __attribute__((aligned(1024))) uint16_t smem[kSmRingBytes / 2];
+    static_assert(sizeof(smem) == kSmRingBytes, "registered LDS figure");
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -262,4 +263,24 @@ extern "C" int pyc_hip_gemm_small_launch(int is_bf16, int b_trans, int tile, int
     }
 #undef PYC_SMALL
     return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+// Registry figures: the 128 KB ring allows one 4-wave workgroup per CU.
+extern "C" int pyc_hip_kinfo_small(int tile, int b_trans, int is_bf16, pyc_hip_kinfo* out) {
+    using namespace pyc;
+    if (!out || (tile != 64 && tile != 128)) return -1;
+    out->threads = 256;
+    out->waves_per_simd = 1;
+    out->lds_bytes = kSmRingBytes;
+    out->name = tile == 64 ? "gemm_small_kernel<64>" : "gemm_small_kernel<128>";
+#define PYC_KI(TY, BT) \
+    out->fn = tile == 64 ? reinterpret_cast<const void*>(&gemm_small_kernel<TY, BT, 64>) \
+                         : reinterpret_cast<const void*>(&gemm_small_kernel<TY, BT, 128>)
+    if (is_bf16) {
+        if (b_trans) PYC_KI(bf16_t, true); else PYC_KI(bf16_t, false);
+    } else {
+        if (b_trans) PYC_KI(f16_t, true); else PYC_KI(f16_t, false);
+    }
+#undef PYC_KI
+    return 0;
 }

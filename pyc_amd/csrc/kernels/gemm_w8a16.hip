@@ -1210,14 +1210,19 @@ int chain_args(pyc::W8ChainArgs& a, const ChainLayout& L, uint8_t* ws, int M, in
 // One workgroup per CU (the LDS ring allows no second one), all resident
 // together. Ring depth: fewer loads in flight shorten the queueing that the
 // step boundary's round trips wait behind (PYC_CHAIN_STAGES overrides).
-int chain_kernel_launch(const pyc::W8ChainArgs& a, hipStream_t st) {
-    using namespace pyc;
+int chain_stages() {
     static int stages = 0;
     if (stages == 0) {
         const char* e = getenv("PYC_CHAIN_STAGES");
         const int v = e ? atoi(e) : 0;
         stages = (v == 4 || v == 5 || v == 6 || v == 8) ? v : 6;
     }
+    return stages;
+}
+
+int chain_kernel_launch(const pyc::W8ChainArgs& a, hipStream_t st) {
+    using namespace pyc;
+    const int stages = chain_stages();
     const dim3 grid(cu_count()), block(kCWaves * kWave);
     if (stages == 4) hipLaunchKernelGGL(w8a16_chain_kernel<4>, grid, block, 0, st, a);
     else if (stages == 5) hipLaunchKernelGGL(w8a16_chain_kernel<5>, grid, block, 0, st, a);
@@ -1377,4 +1382,45 @@ extern "C" int pyc_hip_w8a16_chain_error(int clear) {
         any |= v != 0;
     }
     return any ? 1 : 0;
+}
+
+// Registry figures. LDS: the ring, then the other __shared__ objects as the
+// compiler places them (w8a16_kernel: s_last in a 16-byte slot ahead of the
+// reduction array; the ring kernels: s_last after the ring, the chain's
+// 16-byte aligned k-half partials after it). Waves per SIMD: one workgroup
+// per CU for the ring kernels (LDS) and for the 8-wave register kernel
+// (160 VGPRs leave no room for a second 8-wave workgroup).
+extern "C" int pyc_hip_kinfo_w8a16(int kid, pyc_hip_kinfo* out) {
+    using namespace pyc;
+    if (!out) return -1;
+    switch (kid) {
+        case PYC_KI_W8_LDS:
+            out->name = "w8a16_lds_kernel";
+            out->fn = reinterpret_cast<const void*>(&w8a16_lds_kernel);
+            out->lds_bytes = (size_t)kQStages * kQStageBytes + sizeof(int);
+            out->threads = kQWaves * kWave;
+            out->waves_per_simd = 1;
+            return 0;
+        case PYC_KI_W8_REG:
+            out->name = "w8a16_kernel";
+            out->fn = reinterpret_cast<const void*>(&w8a16_kernel);
+            out->lds_bytes = sizeof(f32x4) + (size_t)kW8Waves * 4 * 2 * kWave * sizeof(f32x4);
+            out->threads = kW8Waves * kWave;
+            out->waves_per_simd = 2;
+            return 0;
+        case PYC_KI_W8_CHAIN: {
+            const int st = chain_stages();
+            out->name = "w8a16_chain_kernel";
+            out->fn = st == 4   ? reinterpret_cast<const void*>(&w8a16_chain_kernel<4>)
+                      : st == 5 ? reinterpret_cast<const void*>(&w8a16_chain_kernel<5>)
+                      : st == 6 ? reinterpret_cast<const void*>(&w8a16_chain_kernel<6>)
+                                : reinterpret_cast<const void*>(&w8a16_chain_kernel<8>);
+            out->lds_bytes = (size_t)st * kQStageBytes + sizeof(f32x4) + 4 * kWave * 2 * sizeof(f32x4);
+            out->threads = kCWaves * kWave;
+            out->waves_per_simd = 2;
+            return 0;
+        }
+        default:
+            return -1;
+    }
 }

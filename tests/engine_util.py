@@ -125,6 +125,24 @@ def ref_available() -> bool:
     return os.path.exists(REF_LIB)
 
 
+# The reference's own engine driving this repository's backend: the
+# reference's engine sources built into one library linked to
+# libpyc_amd_backend.so (oracle/Makefile.ref), whose registry calls bind to
+# the reference's registry.
+REF_HIP_LIB = os.path.join(ROOT, "oracle", "_ref", "libpyc_ref_hip.so")
+BACKEND_LIB = os.path.join(ROOT, "pyc_amd", "lib", "libpyc_amd_backend.so")
+
+
+def ref_on_hip():
+    if "ref_hip" not in _libs:
+        _libs["ref_hip"] = declare(C.CDLL(REF_HIP_LIB))
+    return _libs["ref_hip"]
+
+
+def ref_on_hip_available() -> bool:
+    return os.path.exists(REF_HIP_LIB) and os.path.exists(BACKEND_LIB)
+
+
 def op(kind, name="", dims=(), inputs=(), dtype=abi.DTYPE_F32):
     o = abi.IrOp()
     o.kind = kind

@@ -352,3 +352,29 @@ def test_bf16_passthrough_native():
     mdl.close()
     assert st == 0 and out.tolist() == data.tolist()
     _native(s)
+
+
+def test_matrix_add_with_persistent_only_symbol(monkeypatch):
+    """A GEMM with a folded matrix addend (beta = 1) planned on a symbol that
+    names the persistent kernel alone (here chosen by
+    PYC_CUDA_BF16_GEMM_SYMBOL, as a tuned or promoted choice would be): that
+    kernel refuses beta != 0, so the plan takes the dtype's shape-chosen
+    symbol instead of failing; bf16 4096 x 256 x 4096 + C against the oracle."""
+    monkeypatch.setenv("PYC_CUDA_BF16_GEMM_SYMBOL", "hip_gemm_bf16_nn_256x256_lds")
+    M, K, N = 4096, 256, 4096
+    r = np.random.default_rng(21)
+    x = oracle.f32_to_bf16(r.uniform(-1, 1, (M, K)).astype(np.float32))
+    w = oracle.f32_to_bf16((r.uniform(-1, 1, (K, N)) / 8).astype(np.float32))
+    c = oracle.f32_to_bf16(r.uniform(-1, 1, (M, N)).astype(np.float32))
+    BF = abi.DTYPE_BF16
+    ops = [eu.op(abi.OP_INPUT, "x", (M, K), dtype=BF), eu.op(abi.OP_INPUT, "w", (K, N), dtype=BF),
+           eu.op(abi.OP_INPUT, "c", (M, N), dtype=BF), eu.op(abi.OP_MATMUL, "matmul0", (), (0, 1), dtype=BF),
+           eu.op(abi.OP_ADD, "add0", (), (3, 2), dtype=BF), eu.op(abi.OP_OUTPUT, "out0", (M, N), (4,), dtype=BF)]
+    mdl = eu.Model(eu.mine(), ops, backend=abi.BACKEND_CUDA)
+    assert mdl.status == 0
+    st, (y,), s = mdl.run([x, w, c], [(M, N)], in_dtypes=[BF] * 3, out_dtypes=[BF], out_np_dtype=np.uint16)
+    mdl.close()
+    assert st == 0
+    assert _native(s).endswith(":hip_gemm_bf16_nn"), s.execution_path
+    ref = oracle.gemm_bf16(x, w, False, threads=8) + oracle.bf16_to_f32(c)
+    assert rel_max_err(oracle.bf16_to_f32(y), ref) <= 2e-2
