@@ -184,9 +184,25 @@ pyc_kernel_hardware_family pyc_cuda_current_hardware_family(void) {
     return fam;
 }
 
+/* Number of visible devices, asked of HIP once per process (it does not
+ * change while the process runs; every pyc_run_model checks it). */
+static int device_count(int* count) {
+    static int cached = -1;
+    if (cached < 0) {
+        int n = 0;
+        const hipError_t err = hipGetDeviceCount(&n);
+        if (err != hipSuccess) {
+            return (int)err;
+        }
+        cached = n;
+    }
+    *count = cached;
+    return 0;
+}
+
 static int detect_gpu(char* reason, size_t cap) {
     int count = 0;
-    hipError_t err;
+    int err;
     if (env_true("PYC_CUDA_DISABLE")) {
         set_reason(reason, cap, "disabled_by_env");
         return 0;
@@ -195,12 +211,12 @@ static int detect_gpu(char* reason, size_t cap) {
         set_reason(reason, cap, "cuda_simulated_available");
         return 1;
     }
-    err = hipGetDeviceCount(&count);
-    if (err == hipSuccess && count > 0) {
+    err = device_count(&count);
+    if (err == 0 && count > 0) {
         set_reason(reason, cap, "cuda_runtime_detected");
         return 1;
     }
-    if (err != hipSuccess) {
+    if (err != 0) {
         snprintf(reason, cap, "cuda_runtime_error_%d", (int)err);
     } else {
         set_reason(reason, cap, "cuda_runtime_no_device");
@@ -1739,7 +1755,7 @@ static pyc_cuda_dispatch_status dispatch_locked(const pyc_ir_module* module, con
         int count = 0;
         /* a real device is tried first, also when the simulation flag is set
          * (reference cuda_backend.c:2856-2880) */
-        if (hipGetDeviceCount(&count) == hipSuccess && count > 0) {
+        if (device_count(&count) == 0 && count > 0) {
             native_rc = execute_native(module, inputs, input_count, outputs, output_count, trace, native,
                                        sizeof(native));
             if (native_rc == 0) {
