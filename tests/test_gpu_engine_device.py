@@ -3,8 +3,9 @@ resident tensors of the reference survey's first "next" item). The backend
 binds such tensors to the plan directly (no staging, no host copies) and
 includes their addresses in the graph signature; host and device tensors may
 be mixed. Every run here is checked bit for bit against the same module run
-with host buffers (the same kernels on the same values), and the host runs
-are themselves checked against the oracle in tests/test_gpu_engine.py."""
+with host buffers (the same kernels on the same values) and, directly,
+against the oracle: fp32 within 1e-4 and bf16 / fp8-weight within 2e-2 of
+max|ref| (max|got - ref| / max|ref|)."""
 import ctypes as C
 
 import numpy as np
@@ -13,6 +14,7 @@ import pytest
 import oracle
 from pyc_amd import abi
 from tests import engine_util as eu
+from tests.gpu_util import rel_max_err
 
 pytestmark = pytest.mark.gpu
 
@@ -68,6 +70,7 @@ def test_device_tensors_f32_gemm_bias_relu(gpu):
     assert mdl.status == 0
     st, (host_out,), s = mdl.run([x, w, b], [(M, N)])
     assert st == 0 and s.execution_path.decode().startswith("hip_native")
+    oref = oracle.gemm_bias_relu_f32(x, w, b, relu=True, threads=8)
     X, W, Bv = (torch.from_numpy(t).cuda() for t in (x, w, b))
     Y = torch.full((M, N), float("nan"), device="cuda")
     torch.cuda.synchronize()
@@ -78,6 +81,7 @@ def test_device_tensors_f32_gemm_bias_relu(gpu):
         assert rc == 0, s.execution_path
         paths.append(s.execution_path.decode())
         assert np.array_equal(Y.cpu().numpy(), host_out)
+        assert rel_max_err(Y.cpu().numpy(), oref) <= 1e-4
         assert s.cuda_copy_in_ms < 0.5 and s.cuda_copy_out_ms < 0.5
     mdl.close()
     # one kernel and no copies: launched directly, no graph of one node
@@ -114,6 +118,7 @@ def test_device_tensors_rebind_and_mixed(gpu):
         assert ("graph_replay" if key in seen else "graph_capture") in s.execution_path.decode(), (key, seen)
         seen.add(key)
         assert np.array_equal(Y.cpu().numpy(), ref), f"case {i}"
+        assert rel_max_err(Y.cpu().numpy(), oracle.gemm_bias_relu_f32(x, w, b, relu=True, threads=8)) <= 1e-4
         # host output from the same device inputs
         host_y = np.zeros((M, N), np.float32)
         rc, s = _run(mdl, [_dt(X, abi.DTYPE_F32), _dt(W, abi.DTYPE_F32), _ht(b, abi.DTYPE_F32)],
@@ -146,7 +151,11 @@ def test_device_tensors_bf16_half_bias(gpu):
                  [_dt(Y, abi.DTYPE_BF16)])
     mdl.close()
     assert rc == 0, s.execution_path
-    assert np.array_equal(Y.cpu().numpy().view(np.uint16), ref)
+    got = Y.cpu().numpy().view(np.uint16)
+    assert np.array_equal(got, ref)
+    # oracle: fp32 GEMM of the decoded operands, + bias, ReLU
+    oref = np.maximum(oracle.gemm_bf16(a, w, False, threads=8) + oracle.bf16_to_f32(b)[None, :], 0.0)
+    assert rel_max_err(oracle.bf16_to_f32(got), oref) <= 2e-2
 
 
 def test_device_tensors_decode_chain(gpu):
@@ -187,7 +196,14 @@ def test_device_tensors_decode_chain(gpu):
     mdl.close()
     assert rc == 0, s.execution_path
     assert "hip_w8a16_chain_e4m3" in s.execution_path.decode()
-    assert np.array_equal(Y.cpu().numpy().view(np.uint16), ref)
+    got = Y.cpu().numpy().view(np.uint16)
+    assert np.array_equal(got, ref)
+    # oracle: the fp8-weight layers one after another (bf16 between layers)
+    h = x
+    for l in range(2):
+        wu, su, wd, sd = ins[1 + 4 * l: 5 + 4 * l]
+        h = oracle.w8a16_layer(oracle.w8a16_layer(h, wu, su, True), wd, sd, False)
+    assert rel_max_err(oracle.bf16_to_f32(got), oracle.bf16_to_f32(h)) <= 2e-2
 
 
 def test_device_tensors_never_reach_cpu_executor(gpu, monkeypatch):
