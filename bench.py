@@ -313,6 +313,31 @@ def wl_gemm_f32_cfg1(torch, args):
     return res
 
 
+def hbm_copy_gbs(torch, nbytes: int = 1 << 31, reps: int = 10) -> dict:
+    """Measured HBM bandwidth on this box: a device-to-device copy of `nbytes`
+    (torch's copy kernel), timed over `reps` back-to-back copies by HIP events
+    after three untimed ones; bytes read plus bytes written over the time. The
+    published 8 TB/s stays the roofline's `peak`. torch's copy kernel reaches
+    about 5 TB/s here, below what a streaming kernel reaches (the library's
+    elementwise kernels move 6.3 TB/s), so this is a floor of the achievable
+    rate, reported for reference, not a denominator."""
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    del src, dst
+    return {"value": 2.0 * nbytes / (ms * 1e-3) / 1e9, "unit": "GB/s",
+            "how": f"device-to-device copy of {nbytes >> 20} MiB (torch), read + write bytes, {reps} copies"}
+
+
 def wl_decode_chain(torch, args):
     """Config 5: 8 x [x(32x4096) -> W_up(4096x11008, fp8) -> ReLU -> W_down(11008x4096, fp8)],
     the 16 GEMM steps run as one persistent launch, captured in a hipGraph and replayed."""
@@ -354,6 +379,7 @@ def wl_decode_chain(torch, args):
     weight_bytes = L * (2 * D * F + 4 * (F + D))
     bytes_replay = L * (2 * D * F + 4 * F + 4 * D + M * D * 2 + 2 * M * F * 2 + M * D * 2)
     gbs = bytes_replay / (ms_step * 1e-3) / 1e9
+    copy = hbm_copy_gbs(torch)
     extra = {}
     if not args.no_cpu:
         # CPU leg: the oracle's fp8-weight layer (the reference has no fp8
@@ -389,7 +415,7 @@ def wl_decode_chain(torch, args):
                      "unit": "GB/s", "frac": bytes_replay / (ms_kernel * 1e-3) / 1e9 / PEAK_HBM_GBS,
                      "traffic": load_traffic("decode_chain"), "kernel_ms": ms_kernel,
                      "algorithmic_bytes_per_replay": bytes_replay,
-                     "weight_bytes": weight_bytes},
+                     "weight_bytes": weight_bytes, "measured_copy": copy},
     }
 
 
