@@ -620,44 +620,57 @@ gemm_nt_persist_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
 // between one and two rounds of tiles leaves part of the CUs idle for the
 // whole second round (config 4: 392 tiles on 256 CUs, 120 CUs idle). The
 // launcher then runs one full round of 256-pixel tiles on the persistent
-// kernel and the remaining output pixels here, in tiles of 160 pixels x 256
-// channels, which fit in one round: the second round takes 160/256 of a tile
-// time instead of a whole one.
+// kernel and the remaining output pixels here, in tiles of BM pixels x 256
+// channels, which fit in one round: the second round takes about BM/256 of a
+// tile time instead of a whole one.
 // Same implicit-GEMM view, gather and LDS layout as the persistent kernel;
-// one-shot (a workgroup per tile), 4 waves as 2 x 2, each 80 pixels (5
-// fragments) x 128 channels (8 fragments); BK = 64 stages, three in a ring
-// (A 20 KB + B 32 KB each), loaded by LDS-DMA two stages ahead, one barrier
-// per stage, the loads threaded between the MFMAs. Rows past the last pixel
-// gather the last pixel (never stored).
-constexpr int kTailBM = 160;
+// one-shot (a workgroup per tile), 4 waves as WR x (4/WR): with WR = 1 each
+// wave takes all BM pixels (BM/16 fragments) x 64 channels (4 fragments),
+// with WR = 2 half the pixels x 128 channels (8 fragments). Either way a
+// wave reads the same fragment bytes per stage, so the smaller per-wave tile
+// of the 1 x 4 form is a plain saving (config 4: 242 tiles of 144 pixels in
+// 40.9 us, against 218 tiles of 160 pixels as 2 x 2 in 42.3 us). BK = 64
+// stages, three in a ring (A rows rounded up to a multiple of 32, 20 KB, + B
+// 32 KB each), loaded by LDS-DMA two stages ahead, one barrier per stage, the
+// loads threaded between the MFMAs. Rows past the last pixel gather the last
+// pixel (never stored).
+constexpr int kTailBM = 144;         // pixels per tail tile (the launcher's choice)
+constexpr int kTailWR = 1;           // wave rows of that tile
+constexpr int kTailLoadRows = 160;   // A rows loaded per stage (kTailBM rounded up to 32)
 constexpr int kTailStages = 3;
-constexpr size_t kTailLds = kTailStages * (kTailBM + kD_BN) * 64 * 2;
+constexpr size_t kTailLds = kTailStages * (kTailLoadRows + kD_BN) * 64 * 2;
 
-template <typename T, int EPI>
+template <typename T, int EPI, int BM = kTailBM, int WR = kTailWR>
 __global__ void __launch_bounds__(256, 1)
 conv_tail_kernel(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, uint16_t* __restrict__ Y,
                  int m_base, int M, int N, int K, const float* __restrict__ bias, int tiles_n, ConvGeomP cg) {
     constexpr int BK = 64, CH = 8, NT = 256;
     constexpr int ROWS_PER_LOAD = kWave / CH;          // 8 rows of 128 bytes per DMA instruction
-    constexpr int ALOADS = kTailBM * CH / NT;          // 5 per wave and stage
+    constexpr int LROWS = (BM + 31) / 32 * 32;         // A rows loaded per stage
+    constexpr int ALOADS = LROWS * CH / NT;            // 5 per wave and stage
     constexpr int BLOADS = kD_BN * CH / NT;            // 8
     constexpr int LOADS = ALOADS + BLOADS;             // 13
-    constexpr uint32_t A_BYTES = kTailBM * BK * 2;     // 20 KB
-    constexpr uint32_t STAGE_BYTES = (kTailBM + kD_BN) * BK * 2;
-    constexpr int FM = kTailBM / 2 / 16;               // 5 row fragments per wave
-    static_assert(ALOADS * NT == kTailBM * CH && BLOADS * NT == kD_BN * CH, "DMA split");
+    constexpr uint32_t A_BYTES = LROWS * BK * 2;       // 20 KB
+    constexpr uint32_t STAGE_BYTES = (LROWS + kD_BN) * BK * 2;
+    constexpr int WC = 4 / WR;                         // wave columns
+    constexpr int PXW = BM / WR, CHW = kD_BN / WC;     // pixels and channels per wave
+    constexpr int FM = PXW / 16, FN = CHW / 16;        // fragments per wave
+    constexpr int NCH = CHW / 8;                       // 16-byte chunks of a wave's staged row
+    static_assert(WR * WC == 4 && PXW % 16 == 0 && BM <= LROWS, "tail tile shape");
+    static_assert(ALOADS * NT == LROWS * CH && BLOADS * NT == kD_BN * CH, "DMA split");
     static_assert(kTailStages * STAGE_BYTES <= 160 * 1024, "LDS");
-    static_assert(4 * (kTailBM / 2) * 128 * 2 <= kTailStages * STAGE_BYTES, "epilogue staging");
+    static_assert(4 * PXW * CHW * 2 <= kTailStages * STAGE_BYTES, "epilogue staging");
+    static_assert(FM + FN <= FM * FN && 6 + LOADS <= FM * FN, "loads ride on the MFMA groups");
     __shared__ __attribute__((aligned(1024))) uint16_t smem[kTailStages * STAGE_BYTES / 2];
-    static_assert(sizeof(smem) == kTailLds, "registered LDS figure");
+    static_assert(LROWS != kTailLoadRows || sizeof(smem) == kTailLds, "registered LDS figure");
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WC, wn = wave % WC;
     const int lrow = lane & 15, lgrp = lane >> 4;
     const int tm = blockIdx.x / tiles_n, tn = blockIdx.x - (blockIdx.x / tiles_n) * tiles_n;
-    const int m0 = m_base + tm * kTailBM;
+    const int m0 = m_base + tm * BM;
     const int n0 = tn * kD_BN;
     const int ktiles = K / BK;
 
@@ -725,18 +738,18 @@ conv_tail_kernel(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt
         }
     };
 
-    f32x4 acc[FM][8];
+    f32x4 acc[FM][FN];
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     // Every step issues one stage (clamped to the last: a duplicate into the
     // free slot), so each wave has exactly two stages of loads outstanding at
-    // the top of a step. Per step, 40 groups of two MFMAs in program order
-    // (sched_barrier): the second k half's fragment reads ride on the first
-    // 13 groups and the 13 DMAs of stage kt+2 on groups 6..18, so neither
-    // stalls the MFMA stream.
+    // the top of a step. Per step, FM * FN groups of two MFMAs in program
+    // order (sched_barrier): the second k half's FM + FN fragment reads ride
+    // on the first groups and the 13 DMAs of stage kt+2 on groups 6..18, so
+    // neither stalls the MFMA stream.
     {
         const Tap t0 = tap_of(0), t1 = tap_of(min(1, ktiles - 1));
 #pragma unroll
@@ -749,27 +762,27 @@ conv_tail_kernel(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt
         __syncthreads();        // every wave's part of stage kt is in LDS; stage kt-1 is consumed
         const Tap tn = tap_of(min(kt + 2, ktiles - 1));
         const uint16_t* As = smem + (kt % kTailStages) * (STAGE_BYTES / 2);
-        const uint16_t* Bs = As + kTailBM * BK;
-        u32x4 fa[2][FM], fb[2][8];
+        const uint16_t* Bs = As + LROWS * BK;
+        u32x4 fa[2][FM], fb[2][FN];
         auto rd = [&](int h, int f) {  // fragment f < FM of A, else f - FM of B, k half h
             const int pc = (h * 4 + lgrp) ^ (lrow & 7);
             if (f < FM)
-                fa[h][f] = *reinterpret_cast<const u32x4*>(As + (wm * (kTailBM / 2) + 16 * f + lrow) * BK + pc * 8);
+                fa[h][f] = *reinterpret_cast<const u32x4*>(As + (wm * PXW + 16 * f + lrow) * BK + pc * 8);
             else
-                fb[h][f - FM] = *reinterpret_cast<const u32x4*>(Bs + (wn * 128 + 16 * (f - FM) + lrow) * BK + pc * 8);
+                fb[h][f - FM] = *reinterpret_cast<const u32x4*>(Bs + (wn * CHW + 16 * (f - FM) + lrow) * BK + pc * 8);
         };
 #pragma unroll
-        for (int f = 0; f < FM + 8; ++f) rd(0, f);
+        for (int f = 0; f < FM + FN; ++f) rd(0, f);
 #pragma unroll
-        for (int g = 0; g < FM * 8; ++g) {
+        for (int g = 0; g < FM * FN; ++g) {
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
-                const int p = 2 * g + u;         // product p of the step's 2 * FM * 8
-                const int h = p / (FM * 8), q = p % (FM * 8);
-                const int i = q / 8, j = q % 8;
+                const int p = 2 * g + u;         // product p of the step's 2 * FM * FN
+                const int h = p / (FM * FN), q = p % (FM * FN);
+                const int i = q / FN, j = q % FN;
                 acc[i][j] = mfma16x16x32(fb[h][j], fa[h][i], acc[i][j], T{});
             }
-            if (g < FM + 8) rd(1, g);
+            if (g < FM + FN) rd(1, g);
             if (g >= 6 && g < 6 + LOADS) dma(g - 6, tn);
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -778,15 +791,15 @@ conv_tail_kernel(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt
     __syncthreads();  // every wave is done with the ring; it becomes the C staging area
 
     // epilogue: lane's acc[i][j][e] is (pixel 16i + l%16, channel 16j + 4(l/16) + e)
-    // of the wave's 80 x 128 block; staged row-major (256-byte rows, chunk c
-    // of row r at c ^ (r & 15)) and written as whole 256-byte row segments
+    // of the wave's PXW x CHW block; staged row-major (CHW * 2-byte rows,
+    // chunk c of row r at c ^ (r % NCH)) and written as whole row segments
     constexpr bool has_bias = (EPI & 1) != 0;
     constexpr bool relu = (EPI & 2) != 0;
-    uint16_t* stage = smem + wave * ((kTailBM / 2) * 128);
+    uint16_t* stage = smem + wave * (PXW * CHW);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < FN; ++j) {
         const int c = 16 * j + 4 * lgrp;
-        float4 bv = has_bias ? *reinterpret_cast<const float4*>(bias + n0 + wn * 128 + c) : float4{0.f, 0.f, 0.f, 0.f};
+        float4 bv = has_bias ? *reinterpret_cast<const float4*>(bias + n0 + wn * CHW + c) : float4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
             const int r = 16 * i + lrow;
@@ -799,15 +812,17 @@ conv_tail_kernel(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt
             uint2 packed;
             packed.x = (uint32_t)elem<T>::from_f32(v[0]) | ((uint32_t)elem<T>::from_f32(v[1]) << 16);
             packed.y = (uint32_t)elem<T>::from_f32(v[2]) | ((uint32_t)elem<T>::from_f32(v[3]) << 16);
-            *reinterpret_cast<uint2*>(stage + r * 128 + (((c >> 3) ^ (r & 15)) << 3) + (c & 4)) = packed;
+            *reinterpret_cast<uint2*>(stage + r * CHW + (((c >> 3) ^ (r % NCH)) << 3) + (c & 4)) = packed;
         }
     }
+    constexpr int RPI = kWave / NCH;  // staged rows per read instruction
+    static_assert(PXW % RPI == 0, "epilogue rows");
 #pragma unroll
-    for (int p = 0; p < (kTailBM / 2) / 4; ++p) {
-        const int r = 4 * p + lgrp;
-        const uint4 val = *reinterpret_cast<const uint4*>(stage + r * 128 + ((lrow ^ (r & 15)) << 3));
-        const int gm = m0 + wm * (kTailBM / 2) + r;
-        if (gm < M) *reinterpret_cast<uint4*>(Y + (size_t)gm * N + n0 + wn * 128 + lrow * 8) = val;
+    for (int p = 0; p < PXW / RPI; ++p) {
+        const int r = RPI * p + lane / NCH, lc = lane % NCH;
+        const uint4 val = *reinterpret_cast<const uint4*>(stage + r * CHW + ((lc ^ (r % NCH)) << 3));
+        const int gm = m0 + wm * PXW + r;
+        if (gm < M) *reinterpret_cast<uint4*>(Y + (size_t)gm * N + n0 + wn * CHW + lc * 8) = val;
     }
 }
 
@@ -962,8 +977,8 @@ extern "C" int pyc_hip_conv2d_persist_launch(int is_bf16, int tail, int Nimg, in
     const int tiles_n = Kout / kD_BN;
     int tiles_m = (int)(M / kD_BM);
     // Between one and two rounds of 256-pixel tiles: one full round here and
-    // the remaining pixels in 160-pixel tiles (conv_tail_kernel), when those
-    // fit in one round as well.
+    // the remaining pixels in kTailBM-pixel tiles (conv_tail_kernel), when
+    // those fit in one round as well.
     int m_full = (int)M, tail_tiles = 0;
     if (tail && tail_env && tiles_m * tiles_n > n_cu && tiles_m * tiles_n <= 2 * n_cu && n_cu / tiles_n > 0) {
         const int m1 = (n_cu / tiles_n) * kD_BM;
