@@ -120,3 +120,36 @@ def test_run_model_autotune_every_gemm_shape(gpu, tmp_path, monkeypatch):
     h = oracle.bf16_to_f32(oracle.f32_to_bf16(np.maximum(oracle.gemm_bf16(x, w1, False), 0)))
     ref = oracle.gemm_bf16(oracle.f32_to_bf16(h), w2, False)
     assert rel_max_err(oracle.bf16_to_f32(y), ref) <= 2e-2
+
+
+def test_run_model_autotune_residual_add(gpu, tmp_path, monkeypatch):
+    """Autotune with a matrix addend folded into the GEMM (bf16 4096x4096x256
+    MATMUL + ADD [M,N]): the persistent [K,N] variant, which may win the
+    timing at this shape, takes neither beta = 1 nor the addend, so the plan
+    must fall back to a variant that does. The run stays native (strict
+    mode) and matches the oracle's x @ w + addend."""
+    monkeypatch.setenv("PYC_HIP_STRICT", "1")
+    M, K, N = 4096, 256, 4096
+    r = np.random.default_rng(13)
+    x = oracle.f32_to_bf16(r.uniform(-1, 1, (M, K)).astype(np.float32))
+    w = oracle.f32_to_bf16((r.uniform(-1, 1, (K, N)) / 8).astype(np.float32))
+    add = oracle.f32_to_bf16(r.uniform(-1, 1, (M, N)).astype(np.float32))
+    BF = abi.DTYPE_BF16
+    ops = [engine.op(abi.OP_INPUT, "x", (M, K), dtype=BF), engine.op(abi.OP_INPUT, "w", (K, N), dtype=BF),
+           engine.op(abi.OP_INPUT, "res", (M, N), dtype=BF), engine.op(abi.OP_MATMUL, "matmul0", (), (0, 1), dtype=BF),
+           engine.op(abi.OP_ADD, "add0", (), (3, 2), dtype=BF), engine.op(abi.OP_OUTPUT, "out0", (M, N), (4,), dtype=BF)]
+    db = tmp_path / "tune.db"
+    mdl = engine.Model(ops, backend=abi.BACKEND_CUDA, enable_autotune=1, autotune_db_path=str(db).encode())
+    assert mdl.status == 0
+    y = np.zeros((M, N), np.uint16)
+    for _ in range(2):  # tune and capture, then replay
+        rc, st = mdl.run([engine.host_tensor(a, BF) for a in (x, w, add)], [engine.host_tensor(y, BF)])
+        assert rc == 0 and st.execution_path.decode().startswith("hip_native"), st.execution_path
+    path = st.execution_path.decode()
+    mdl.close()
+    assert st.autotune_saved == 1
+    timed = {ln.split("|")[2] for ln in db.read_text().splitlines() if ln.strip()}
+    assert "hip_gemm_bf16_nn_256x256" in timed, timed  # the persistent variant was a candidate
+    assert not path.endswith(":hip_gemm_bf16_nn_256x256"), path
+    ref = oracle.gemm_bf16(x, w, False, threads=8) + oracle.bf16_to_f32(add)
+    assert rel_max_err(oracle.bf16_to_f32(y), ref) <= 2e-2
