@@ -694,6 +694,102 @@ def wl_engine_bf16(torch, args):
     }
 
 
+def wl_engine_chain(torch, args):
+    """BASELINE config 5 as a module through pyc_compile_model / pyc_run_model:
+    x -> 8 x (fp8 MATMUL up + ReLU, fp8 MATMUL down) -> y, with every weight,
+    scale and activation resident in device memory. The backend plans the 16
+    fp8 steps as one chain launch; a step of this workload is one
+    pyc_run_model call (launch and wait), timed by wall clock, so the figure
+    includes the engine's per-call host work on top of the kernel. The output
+    is compared bit for bit with a direct pyc_hip_w8a16_chain_dispatch of the
+    same chain."""
+    import pyc_amd
+    from pyc_amd import abi, engine
+    os.environ["PYC_HIP_STRICT"] = "1"
+    L, M, D, F = 8, 32, 4096, 11008
+    g = torch.Generator(device="cuda").manual_seed(9)
+    x = torch.randn((M, D), generator=g, device="cuda").to(torch.bfloat16)
+    weights = []
+    for l in range(L):
+        gl = torch.Generator(device="cuda").manual_seed(10 + l)
+        w_up = torch.randn((D, F), generator=gl, device="cuda") * np.sqrt(2.0 / D)
+        w_dn = torch.randn((F, D), generator=gl, device="cuda") * np.sqrt(2.0 / F)
+        for w in (w_up, w_dn):  # per-output-column scale, stored [N,K] e4m3fn
+            s = (w.abs().amax(0) / 448.0).clamp_min(1e-30)
+            q = (w / s).t().contiguous().to(torch.float8_e4m3fn).view(torch.uint8)
+            weights += [q, s.float().contiguous()]
+        del w_up, w_dn
+    BF, F8, F32 = abi.DTYPE_BF16, abi.DTYPE_FP8_E4M3, abi.DTYPE_F32
+    ops = [engine.op(abi.OP_INPUT, "x", (M, D), dtype=BF)]
+    ins = [engine.device_tensor(x, BF)]
+    cur = 0
+    for l in range(L):
+        qu, su, qd, sd = weights[4 * l:4 * l + 4]
+        base = len(ops)
+        ops += [engine.op(abi.OP_INPUT, f"wu{l}", (F, D), dtype=F8), engine.op(abi.OP_INPUT, f"su{l}", (F,)),
+                engine.op(abi.OP_INPUT, f"wd{l}", (D, F), dtype=F8), engine.op(abi.OP_INPUT, f"sd{l}", (D,))]
+        ins += [engine.device_tensor(qu, F8), engine.device_tensor(su, F32),
+                engine.device_tensor(qd, F8), engine.device_tensor(sd, F32)]
+        ops += [engine.op(abi.OP_MATMUL, f"up{l}", (), (cur, base, base + 1), dtype=BF),
+                engine.op(abi.OP_RELU, f"relu{l}", (), (base + 4,), dtype=BF),
+                engine.op(abi.OP_MATMUL, f"down{l}", (), (base + 5, base + 2, base + 3), dtype=BF)]
+        cur = base + 6
+    ops.append(engine.op(abi.OP_OUTPUT, "y", (M, D), (cur,), dtype=BF))
+    y = torch.empty((M, D), dtype=torch.bfloat16, device="cuda")
+    model = engine.Model(ops, backend=abi.BACKEND_CUDA)
+    if model.status != 0:
+        raise RuntimeError(f"pyc_compile_model failed: {model.status}")
+    run = model.bind(ins, [engine.device_tensor(y, BF)])
+    torch.cuda.synchronize()
+
+    def call():
+        rc, st = run()
+        if rc != 0:
+            raise RuntimeError(f"pyc_run_model failed ({rc}): {st.execution_path.decode()}")
+        return st
+
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < args.settle_ms:
+        call()
+    for _ in range(args.warmup):
+        call()
+    stats, wall = [], []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        t1 = time.perf_counter()
+        stats.append(call())
+        wall.append((time.perf_counter() - t1) * 1e3)
+    ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    eng = engine.run_stats_json(stats, wall, model)
+    kernel_ms = engine_device_kernel_ms(call, min(args.steps, 20))
+    model.close()
+    if "hip_w8a16_chain_e4m3" not in eng["execution_path"]:
+        raise RuntimeError(f"engine run did not take the chain launch: {eng['execution_path']}")
+    # the same chain through the direct entry point: identical bits expected
+    chain_layers = []
+    for l in range(L):
+        qu, su, qd, sd = weights[4 * l:4 * l + 4]
+        chain_layers += [(qu, su, True), (qd, sd, False)]
+    y_direct = torch.empty_like(y)
+    pyc_amd.w8a16_chain(x, chain_layers, y_direct)
+    torch.cuda.synchronize()
+    same = bool(torch.equal(y.view(torch.int16), y_direct.view(torch.int16)))
+    bytes_replay = L * (2 * D * F + 4 * F + 4 * D + M * D * 2 + 2 * M * F * 2 + M * D * 2)
+    return {
+        "value": bytes_replay / (ms_step * 1e-3) / 1e9, "unit": "GB/s", "ms_per_step": ms_step,
+        "dtype": "fp8-e4m3 weights, bf16 activations",
+        "config": {"workload": "engine_pyc_run_model_decode_chain_8x(32x4096x11008)", "tensors": "device-resident",
+                   "module": "x, 8 x (matmul_fp8 + relu, matmul_fp8), y"},
+        "roofline": {"bound": "hbm", "achieved": bytes_replay / (kernel_ms * 1e-3) / 1e9, "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": bytes_replay / (kernel_ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                     "traffic": load_traffic("decode_chain"), "kernel_ms": kernel_ms},
+        "latency_ms": eng.pop("latency_ms"),
+        "engine": eng,
+        "matches_direct_chain": same,
+        "vs_baseline": None,
+    }
+
+
 def _eltwise_line(name, config, nbytes, ms_step, ms_kernel):
     return {
         "value": nbytes / (ms_step * 1e-3) / 1e9, "unit": "GB/s", "ms_per_step": ms_step, "dtype": "bf16",
@@ -736,7 +832,7 @@ def wl_layernorm(torch, args):
 
 WORKLOADS = {"gemm_bf16": wl_gemm_bf16, "gemm_bf16_nn": wl_gemm_bf16_nn, "gemm_f32_cfg1": wl_gemm_f32_cfg1, "decode_chain": wl_decode_chain,
              "attention": wl_attention, "conv": wl_conv, "engine_cfg1": wl_engine_cfg1,
-             "engine_bf16": wl_engine_bf16,
+             "engine_bf16": wl_engine_bf16, "engine_chain": wl_engine_chain,
              "gelu": wl_gelu, "layernorm": wl_layernorm}
 
 
@@ -804,7 +900,7 @@ def main() -> int:
     line["latency_ms"] = latency
     line["settle"] = settled
     for k in ("cpu_baseline", "cpu_baseline_1thread", "parity_sample_max_rel_err", "speedup_vs_cpu", "baseline_ref",
-              "engine"):
+              "engine", "matches_direct_chain"):
         if k in res:
             line[k] = res[k]
     line.update(nested)

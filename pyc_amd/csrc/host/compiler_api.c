@@ -56,6 +56,13 @@
 #define CACHE_MAX 32
 #define CANDIDATE_MAX 32
 #define LOG_MAX 2048
+/* Inputs and outputs a run may have and still take the stable-repeat fast
+ * path. The reference caps it at PYC_IR_MAX_INPUTS (8): every module its GPU
+ * path runs has at most three inputs. Multi-op modules here have more (the
+ * 8-layer fp8 decode chain has 33), and a repeat of one of them skips the
+ * same per-run work (fingerprint, shape bucket, controller, kernel
+ * coselection). Up to 8 the behaviour is the reference's. */
+#define REPEAT_MAX 64
 
 typedef struct {
     int valid;
@@ -125,8 +132,8 @@ struct pyc_compiled_model {
     uint64_t last_hash;
     char last_bucket[64];
     char last_signature[SIG_MAX];
-    pyc_tensor last_in[PYC_IR_MAX_INPUTS];
-    pyc_tensor last_out[PYC_IR_MAX_INPUTS];
+    pyc_tensor last_in[REPEAT_MAX];
+    pyc_tensor last_out[REPEAT_MAX];
     size_t last_in_count, last_out_count;
     float* workspace[PYC_IR_MAX_OPS];
     size_t workspace_bytes[PYC_IR_MAX_OPS];
@@ -1757,7 +1764,7 @@ pyc_status pyc_run_model(pyc_compiled_model* model, const pyc_tensor* inputs, si
 
     /* stable-repeat fast path: identical descriptors as the previous good run */
     if (model->last_valid && !model->options.enable_speculative_plans && !model->options.enable_phantom_graph &&
-        input_count <= PYC_IR_MAX_INPUTS && output_count <= PYC_IR_MAX_INPUTS &&
+        input_count <= REPEAT_MAX && output_count <= REPEAT_MAX &&
         same_descriptors(inputs, input_count, model->last_in, model->last_in_count) &&
         same_descriptors(outputs, output_count, model->last_out, model->last_out_count)) {
         shape_cached = 1;
@@ -1841,8 +1848,8 @@ pyc_status pyc_run_model(pyc_compiled_model* model, const pyc_tensor* inputs, si
         model->last_hash = hash;
         copy_str(model->last_bucket, sizeof(model->last_bucket), bucket);
         copy_str(model->last_signature, sizeof(model->last_signature), sig);
-        model->last_in_count = input_count <= PYC_IR_MAX_INPUTS ? input_count : 0;
-        model->last_out_count = output_count <= PYC_IR_MAX_INPUTS ? output_count : 0;
+        model->last_in_count = input_count <= REPEAT_MAX ? input_count : 0;
+        model->last_out_count = output_count <= REPEAT_MAX ? output_count : 0;
         for (i = 0; i < model->last_in_count; ++i) model->last_in[i] = inputs[i];
         for (i = 0; i < model->last_out_count; ++i) model->last_out[i] = outputs[i];
     } else if (error) {
