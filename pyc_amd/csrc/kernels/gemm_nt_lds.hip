@@ -660,7 +660,9 @@ conv_tail_kernel(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt
     static_assert(ALOADS * NT == LROWS * CH && BLOADS * NT == kD_BN * CH, "DMA split");
     static_assert(kTailStages * STAGE_BYTES <= 160 * 1024, "LDS");
     static_assert(4 * PXW * CHW * 2 <= kTailStages * STAGE_BYTES, "epilogue staging");
-    static_assert(FM + FN <= FM * FN && 6 + LOADS <= FM * FN, "loads ride on the MFMA groups");
+    // the second k half's fragments are all read (one per group, from group 0)
+    // before its first MFMA (group FM * FN / 2), and the DMAs fit in the step
+    static_assert(FM + FN <= FM * FN / 2 && 6 + LOADS <= FM * FN, "loads ride on the MFMA groups");
     __shared__ __attribute__((aligned(1024))) uint16_t smem[kTailStages * STAGE_BYTES / 2];
     static_assert(LROWS != kTailLoadRows || sizeof(smem) == kTailLds, "registered LDS figure");
 
