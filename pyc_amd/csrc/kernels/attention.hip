@@ -240,20 +240,35 @@ attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
         ivrs = make_buf_rsrc(Vp + b, head_bytes);
     };
     set_issue_head();  // the grid is no larger than the number of units
-    auto issue_next = [&]() {
+    // One entry's loads are issued in three parts: issue_begin sets the
+    // block offset and ring slot, issue_one(x) issues load x of the
+    // 2 * DMAS (K and V alternating), issue_end moves the cursor on (and may
+    // switch the descriptors to the next head, so it comes after the last
+    // issue_one of the entry). The M phase spreads the issue_one calls over
+    // its MFMA steps.
+    uint32_t isb = 0;
+    auto issue_begin = [&]() {
         if (ic.i >= 0 && ie < ic.n) iboff = (uint32_t)ie * kAttnBK * D * 2;
-        const uint32_t sb = (inext % kAttnRing) * 2 * TILE * 2;
-#pragma unroll
-        for (int jj = 0; jj < DMAS; ++jj) {
-            lds_dma_buf_b128(ikrs, kvo[jj] + iboff, 0u, klds[jj] + sb);
-            lds_dma_buf_b128(ivrs, vvo[jj] + iboff, 0u, klds[jj] + sb + TILE * 2);
-        }
+        isb = (inext % kAttnRing) * 2 * TILE * 2;
+    };
+    auto issue_one = [&](int x) {
+        const int jj = x >> 1;
+        if (x & 1) lds_dma_buf_b128(ivrs, vvo[jj] + iboff, 0u, klds[jj] + isb + TILE * 2);
+        else lds_dma_buf_b128(ikrs, kvo[jj] + iboff, 0u, klds[jj] + isb);
+    };
+    auto issue_end = [&]() {
         ++inext;
         if (ic.i >= 0 && ++ie > ic.n) {
             advance(ic);
             ie = 0;
             if (ic.i >= 0) set_issue_head();
         }
+    };
+    auto issue_next = [&]() {
+        issue_begin();
+#pragma unroll
+        for (int x = 0; x < 2 * DMAS; ++x) issue_one(x);
+        issue_end();
     };
 
     // Per-lane LDS element offsets of the fragment reads. The K rows a lane
@@ -333,6 +348,7 @@ attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
         constexpr int NPV = (4 * DT) / KK;
         static_assert(NPV * KK == 4 * DT, "PV steps per S step");
         auto m_phase = [&](auto ds_tag, auto dp_tag, uint32_t es, uint32_t ep) {
+            static_assert(2 * DMAS <= KK, "one load per MFMA step at most");
             constexpr bool DS = decltype(ds_tag)::value, DP = decltype(dp_tag)::value;
             // slot offsets made opaque so that the per-slot fragment
             // addresses are formed here (one add each) instead of being
@@ -375,6 +391,7 @@ attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
                     load(st + 1, (st + 1) & 1);
                     __builtin_amdgcn_sched_group_barrier(0x100, NRD, 0);  // DS reads
                 }
+                if (st < 2 * DMAS) issue_one(st);  // this M phase's share of the next entry
                 __builtin_amdgcn_sched_group_barrier(0x008, NMF, 0);      // MFMAs
                 if constexpr (DS) {
 #pragma unroll
@@ -493,13 +510,18 @@ attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kp,
             // the remaining issue cycles (left to age order, the older
             // group's softmax would delay the younger group's MFMAs).
             __builtin_amdgcn_s_setprio(2);
-            issue_next();
+            issue_begin();
             // wave-uniform. The last PV of a wave (k = n_w - 1) also computes
             // an S that is never used: its slot holds finite data (a real
             // block or a dummy entry), and one variant fewer keeps the
             // register allocation tight.
             if (k < 0) m_phase(yes{}, no{}, e0, e0);
             else if (k < n_w) m_phase(yes{}, yes{}, e0 + (uint32_t)(k + 1), e0 + (uint32_t)k);
+            else {
+#pragma unroll
+                for (int x = 0; x < 2 * DMAS; ++x) issue_one(x);
+            }
+            issue_end();
             wait_vmem_le<2 * DMAS>();  // own part of the next entry (and any Q prefetch) landed
             __builtin_amdgcn_s_setprio(0);
             __syncthreads();
