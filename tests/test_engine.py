@@ -590,3 +590,53 @@ def test_hip_autotune_without_gpu():
     import torch
     if not torch.cuda.is_available():
         assert f(abi.DTYPE_BF16, 8, 8, 8, 1, syms, 64, ms, 4) == 0
+
+
+def test_stable_repeat_fastpath_many_inputs(monkeypatch):
+    """A module with more inputs than the reference's stable-repeat cap (8
+    inputs; this engine takes the fast path up to 64): repeats with identical
+    descriptors take the fast path, which must still read the inputs' current
+    contents, and a changed descriptor (a new buffer, a wrong shape) must go
+    through the full guard path again. The reference engine, which never
+    takes the fast path at this size, gives the same statuses and outputs."""
+    monkeypatch.setenv("PYC_CUDA_DISABLE", "1")  # the GPU backend's CPU fallback, with or without a device
+    n = 12
+    ops = [eu.op(abi.OP_INPUT, f"x{i}", (4,)) for i in range(n)]
+    cur = 0
+    for i in range(1, n):
+        ops.append(eu.op(abi.OP_ADD, f"a{i}", (), (cur, i)))
+        cur = len(ops) - 1
+    ops.append(eu.op(abi.OP_OUTPUT, "o", (4,), (cur,)))
+    results = {}
+    for name in LIBS if eu.ref_available() else ["mine"]:
+        L = lib(name)
+        mdl = eu.Model(L, ops, backend=abi.BACKEND_CUDA)
+        xs = [np.full(4, float(i + 1), np.float32) for i in range(n)]
+        y = np.zeros(4, np.float32)
+
+        def run(inputs):
+            ins = (abi.Tensor * len(inputs))(*[eu.tensor(a, abi.DTYPE_F32) for a in inputs])
+            outs = (abi.Tensor * 1)(eu.tensor(y, abi.DTYPE_F32))
+            s = abi.RunStats()
+            return L.pyc_run_model(mdl.h, ins, len(inputs), outs, 1, C.byref(s)), y.copy()
+
+        seq = [run(xs) for _ in range(3)]
+        xs[5][:] = 100.0  # same buffer, new contents
+        seq.append(run(xs))
+        xs[7] = np.full(4, -3.0, np.float32)  # a new buffer
+        seq.append(run(xs))
+        bad = list(xs)
+        bad[3] = np.zeros(5, np.float32)  # wrong shape
+        seq.append(run(bad))
+        seq.append(run(xs))
+        seq.append(run(xs))
+        mdl.close()
+        total = float(sum(range(1, n + 1)))
+        want = [total] * 3 + [total - 6 + 100, total - 6 + 100 - 8 - 3]
+        for (st, out), w in zip(seq[:5], want):
+            assert st == 0 and np.allclose(out, w), (name, st, out, w)
+        assert seq[5][0] != 0, name
+        assert all(st == 0 and np.allclose(out, want[-1]) for st, out in seq[6:]), name
+        results[name] = [st for st, _ in seq]
+    if "ref" in results:
+        assert results["mine"] == results["ref"]
