@@ -24,6 +24,10 @@ PROGRAMS = sorted(os.listdir(CTEST_DIR)) if os.path.isdir(CTEST_DIR) else []
 # reads the golden fusion output from the reference checkout, which only the
 # build host has
 NEEDS_SOURCES = {"test_pass_golden"}
+# Exit codes that assert wall-clock budgets rather than behaviour: under the
+# sanitizers' slowdown a cache-hit compile can miss test_compile_cache's 1 ms
+# budget (exit 6). The sanitized run still has to end without a report.
+SANITIZED_TIMING_EXITS = {"test_compile_cache": {6}}
 
 
 def _run(name, tmp_path, sanitized=False):
@@ -39,8 +43,10 @@ def _run(name, tmp_path, sanitized=False):
                    ASAN_OPTIONS="detect_leaks=1:halt_on_error=1", UBSAN_OPTIONS="halt_on_error=1:print_stacktrace=1")
     r = subprocess.run([os.path.join(CTEST_DIR, name)], cwd=tmp_path, env=env, capture_output=True, text=True,
                        timeout=120)
-    assert r.returncode == 0, f"{name} exited {r.returncode}:\n{r.stdout[-2000:]}\n{r.stderr[-2000:]}"
     assert "Sanitizer" not in r.stderr and "runtime error" not in r.stderr, r.stderr[-3000:]
+    if sanitized and r.returncode in SANITIZED_TIMING_EXITS.get(name, ()):
+        return
+    assert r.returncode == 0, f"{name} exited {r.returncode}:\n{r.stdout[-2000:]}\n{r.stderr[-2000:]}"
     assert "ok" in r.stdout.strip().splitlines()[-1], r.stdout[-500:]
 
 
