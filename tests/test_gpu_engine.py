@@ -359,9 +359,11 @@ def test_matrix_add_with_persistent_only_symbol(monkeypatch):
     names the persistent kernel alone (here chosen by
     PYC_CUDA_BF16_GEMM_SYMBOL, as a tuned or promoted choice would be): that
     kernel refuses beta != 0, so the plan takes the dtype's shape-chosen
-    symbol instead of failing; bf16 4096 x 256 x 4096 + C against the oracle."""
+    symbol instead of failing; bf16 4352 x 256 x 4096 + C against the oracle.
+    The shape is one no other test autotunes: a tuned winner for a shape is
+    kept per process and takes precedence over the env-selected symbol."""
     monkeypatch.setenv("PYC_CUDA_BF16_GEMM_SYMBOL", "hip_gemm_bf16_nn_256x256_lds")
-    M, K, N = 4096, 256, 4096
+    M, K, N = 4352, 256, 4096
     r = np.random.default_rng(21)
     x = oracle.f32_to_bf16(r.uniform(-1, 1, (M, K)).astype(np.float32))
     w = oracle.f32_to_bf16((r.uniform(-1, 1, (K, N)) / 8).astype(np.float32))
