@@ -233,7 +233,9 @@ def test_promoted_unit_epilogue_symbol_not_used_for_matrix_add(monkeypatch):
 def test_device_inputs_from_another_stream_without_graph(monkeypatch, gpu):
     """PYC_CUDA_ENABLE_GRAPH_REPLAY=0: inputs (and a bf16 bias the backend
     reads back to convert) are written by a copy queued on another
-    non-blocking stream behind a long kernel chain; the run must see them."""
+    non-blocking stream behind a long kernel chain and handed over to the
+    default stream with wait_stream (no host wait); the run, ordered after the
+    default stream, must see them."""
     torch = gpu
     monkeypatch.setenv("PYC_CUDA_ENABLE_GRAPH_REPLAY", "0")
     monkeypatch.setenv("PYC_HIP_STRICT", "1")
@@ -258,6 +260,9 @@ def test_device_inputs_from_another_stream_without_graph(monkeypatch, gpu):
             big = big @ big / 64.0  # ~4 ms of work ahead of the copies
         for d, s_ in zip(dst, src):
             d.copy_(s_)
+    # the hand-over to the default stream, without a host wait: the run is
+    # ordered after the default stream's work, which now includes the copies
+    torch.cuda.current_stream().wait_stream(side)
     I = (abi.Tensor * 3)(*[_dt(t, BF) for t in dst])
     O = (abi.Tensor * 1)(_dt(Y, BF))
     stats = abi.RunStats()
