@@ -63,6 +63,9 @@ int pyc_hip_w8a16_chain_supported(int M, int nsteps, const int* N, const int* K)
 int pyc_hip_w8a16_chain_error_enqueue(int* host_dst, void* stream);
 /* completion word of a run (run_signal.hip) */
 int pyc_hip_run_signal_enqueue(uint32_t* host_word, uint32_t seq, void* stream);
+/* the fp32 GEMM's own completion store (gemm_f32.hip) */
+void pyc_hip_gemm_f32_signal_arm(uint32_t* host_word, uint32_t* dev_count, uint32_t seq);
+int pyc_hip_gemm_f32_signal_taken(void);
 /* 1 when a GEMM symbol takes alpha = 1, beta = 0 only; 1 when it names the
  * persistent kernel alone, which refuses beta != 0 and unaligned C or bias
  * (hip_kernels.c) */
@@ -807,6 +810,7 @@ static struct {
     int* chain_err;                /* pinned copy of the chain kernel's timeout word */
     uint32_t* done_word;           /* pinned, host-coherent completion word (run_signal.hip) */
     uint32_t done_seq;             /* sequence number of the last run that signalled */
+    uint32_t* done_count;          /* device arrival counter of a kernel that signals itself */
     uint64_t upload_module;        /* module whose static inputs val[] holds (uploaded[]) */
     /* graph replay: one executable graph per run signature, least recently
      * used one replaced */
@@ -880,6 +884,9 @@ static void ws_release(void) {
     if (g_ws.done_word) {
         (void)hipHostFree(g_ws.done_word);
     }
+    if (g_ws.done_count) {
+        (void)hipFree(g_ws.done_count);
+    }
     if (g_ws.ready) {
         (void)hipEventDestroy(g_ws.ev0);
         (void)hipEventDestroy(g_ws.ev1);
@@ -913,6 +920,14 @@ static int ws_init(void) {
     }
     *g_ws.done_word = 0;
     g_ws.done_seq = 0;
+    /* the signalling kernel's counters: 9 x 256 bytes (gemm_f32.hip) */
+    if (hipMalloc((void**)&g_ws.done_count, 4096) != hipSuccess) {
+        g_ws.done_count = NULL;
+        return -1;
+    }
+    if (hipMemset(g_ws.done_count, 0, 4096) != hipSuccess) {
+        return -1;
+    }
     g_ws.ready = 1;
     return 0;
 }
@@ -1060,13 +1075,20 @@ static uint64_t fnv(uint64_t h, const void* p, size_t n) {
 
 /* Enqueue the kernels of the plan on the workspace stream; vp[v] is the
  * device storage of value v (workspace, or the caller's device tensor). */
-static int enqueue_steps(const pyc_ir_module* m, const hip_plan* plan, void* const* vp, char* why, size_t why_cap) {
+/* Enqueues the plan's kernels on the backend stream. arm_seq != 0: the run's
+ * last kernel is also its last work on the stream, and when that kernel can
+ * store the completion word itself (the fp32 LDS-DMA GEMM) it is launched so;
+ * *signalled says whether it was. */
+static int enqueue_steps(const pyc_ir_module* m, const hip_plan* plan, void* const* vp, uint32_t arm_seq,
+                         int* signalled, char* why, size_t why_cap) {
     size_t s;
     void* st_stream = (void*)g_ws.stream;
+    *signalled = 0;
     for (s = 0; s < plan->nsteps; ++s) {
         const hip_step* st = &plan->steps[s];
         void* out = vp[st->out];
         const size_t clen = (size_t)st->chain_len;
+        const int arm = arm_seq != 0 && s + 1 == plan->nsteps && st->kind == ST_GEMM && st->dtype == PYC_DTYPE_F32;
         if (clen >= 2) {
             /* the whole run of fp8-weight steps in one launch */
             const void* wq[HIP_CHAIN_MAX_STEPS];
@@ -1110,6 +1132,9 @@ static int enqueue_steps(const pyc_ir_module* m, const hip_plan* plan, void* con
             }
             beta = 1.0f;
         }
+        if (arm) {
+            pyc_hip_gemm_f32_signal_arm(g_ws.done_word, g_ws.done_count, arm_seq);
+        }
         switch (st->kind) {
             case ST_GEMM:
                 rc = pyc_hip_gemm_dispatch(st->symbol, st->m, st->n, st->k, vp[st->in[0]],
@@ -1149,6 +1174,9 @@ static int enqueue_steps(const pyc_ir_module* m, const hip_plan* plan, void* con
             }
             default:
                 break;
+        }
+        if (arm) {
+            *signalled = pyc_hip_gemm_f32_signal_taken() && rc == 0;
         }
         if (rc != 0) {
             snprintf(why, why_cap, "hip_kernel_failed:%s", st->symbol);
@@ -1401,6 +1429,16 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
      * records cost ~4.4 us per run on MI355X, a third of a small GEMM's call. */
     const int use_ev = trace && env_true("PYC_HIP_KERNEL_EVENTS");
     double t_enq = 0.0;
+    /* completion word: see the wait below */
+    int signal = !use_ev && !has_chain;
+    int signalled = 0;
+    uint32_t done_seq = 0;
+    for (i = 0; signal && i < plan.n_outputs; ++i) {
+        signal = dev_out[i] || skip_out;
+    }
+    if (signal) {
+        done_seq = ++g_ws.done_seq == 0 ? ++g_ws.done_seq : g_ws.done_seq; /* 0 is the initial word */
+    }
 
     /* host -> pinned staging */
     t0 = now_ms();
@@ -1454,7 +1492,13 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
             }
             if (rc == 0) {
                 const double te = now_ms();
-                rc = enqueue_steps(m, &plan, vp, why, why_cap);
+                /* the kernel may carry the completion word when nothing
+                 * follows it on the stream */
+                int arm = signal && !use_graph;
+                for (i = 0; arm && i < plan.n_outputs; ++i) {
+                    arm = !(dev_out[i] && out_d2d[i]);
+                }
+                rc = enqueue_steps(m, &plan, vp, arm ? done_seq : 0u, &signalled, why, why_cap);
                 if (!use_graph) {
                     t_enq += now_ms() - te;
                 }
@@ -1522,17 +1566,14 @@ static int execute_native(const pyc_ir_module* m, const pyc_tensor* inputs, size
     }
     /* The wait. A run whose results all stay in device memory (no copy into
      * host staging, no chain timeout word to read back, no timing events)
-     * waits on the completion word that run_signal.hip stores behind its work:
-     * ~4.6 us sooner after the last kernel than hipStreamSynchronize on this
-     * stack. The others synchronize the stream. */
+     * waits on a completion word stored behind its work: by its last kernel
+     * itself where that kernel can (signalled), else by run_signal.hip's
+     * one-lane kernel; either is ~4.6 us sooner after the work than
+     * hipStreamSynchronize on this stack. The others synchronize the stream. */
     {
-        int signal = !use_ev && !has_chain;
-        for (i = 0; signal && i < plan.n_outputs; ++i) {
-            signal = dev_out[i] || skip_out;
-        }
         if (signal) {
-            const uint32_t seq = ++g_ws.done_seq == 0 ? ++g_ws.done_seq : g_ws.done_seq; /* 0 is the initial word */
-            if (pyc_hip_run_signal_enqueue(g_ws.done_word, seq, g_ws.stream) != 0 || wait_done_word(seq) != 0) {
+            if ((!signalled && pyc_hip_run_signal_enqueue(g_ws.done_word, done_seq, g_ws.stream) != 0) ||
+                wait_done_word(done_seq) != 0) {
                 snprintf(why, why_cap, "hip_sync_failed");
                 return -1;
             }

@@ -88,6 +88,50 @@ def test_device_tensors_f32_gemm_bias_relu(gpu):
     assert all(p.startswith("hip_native:") for p in paths), paths
 
 
+@pytest.mark.parametrize("M,K,N", [(1024, 1024, 1024), (200, 136, 72)])
+def test_device_tensors_back_to_back_runs_read_at_once(gpu, M, K, N):
+    """Runs with device tensors return on a completion word: at 1024^3 the
+    fp32 GEMM stores it itself once every workgroup's C is complete (its last
+    waves may still be exiting); at 200x136x72, off the LDS-DMA kernel's tile
+    multiples, a one-lane kernel stores it behind the GEMM. Each run's output is
+    read by a torch kernel on the default stream as soon as the call returns,
+    with no synchronization between, and every run's inputs differ from the
+    previous one's (written in place on the default stream before the call),
+    so a stale or partial output fails the bit-for-bit check against the
+    host-buffer run of the same inputs. 12 runs exercise the counter's re-arm."""
+    torch = gpu
+    r = np.random.default_rng(7)
+    mdl = _gemm_module(M, K, N)
+    assert mdl.status == 0
+    cases = []
+    for _ in range(3):
+        x, w = (r.uniform(-1, 1, sh).astype(np.float32) for sh in ((M, K), (K, N)))
+        b = r.uniform(-1, 1, N).astype(np.float32)
+        st, (ref,), _ = mdl.run([x, w, b], [(M, N)])
+        assert st == 0
+        cases.append((torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda(), torch.from_numpy(b).cuda(), ref.copy()))
+    assert rel_max_err(cases[0][3], oracle.gemm_bias_relu_f32(*(t.cpu().numpy() for t in cases[0][:3]), relu=True,
+                                                               threads=8)) <= 1e-4
+    X, W, Bv = (torch.empty_like(t) for t in cases[0][:3])
+    Y = torch.full((M, N), float("nan"), device="cuda")
+    got = []
+    torch.cuda.synchronize()
+    for i in range(12):
+        x, w, b, _ = cases[i % 3]
+        X.copy_(x)
+        W.copy_(w)
+        Bv.copy_(b)
+        rc, s = _run(mdl, [_dt(X, abi.DTYPE_F32), _dt(W, abi.DTYPE_F32), _dt(Bv, abi.DTYPE_F32)],
+                     [_dt(Y, abi.DTYPE_F32)])
+        assert rc == 0, s.execution_path
+        assert s.execution_path.decode().startswith("hip_native:"), s.execution_path
+        got.append(Y.clone())
+    torch.cuda.synchronize()
+    for i, g in enumerate(got):
+        assert np.array_equal(g.cpu().numpy(), cases[i % 3][3]), f"run {i}"
+    mdl.close()
+
+
 def test_device_tensors_rebind_and_mixed(gpu):
     """New device addresses capture a new graph (a graph bakes in the addresses
     it was captured with); host and device tensors in one call; a host run
