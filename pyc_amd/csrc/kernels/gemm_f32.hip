@@ -422,16 +422,17 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
     }
 }
 
-// Completion signal armed by the run path for its last kernel (the backend
-// drives one run at a time): the next LDS-DMA launch carries it, and the run
-// asks afterwards whether one did.
+// Completion signal armed by the run path for its last kernel: the next
+// LDS-DMA launch on the same thread carries it, and the run asks afterwards
+// whether one did. Per thread, so that a GEMM another thread dispatches
+// meanwhile cannot take it.
 struct F32Signal {
     uint32_t* word = nullptr;   // pinned host word (hipHostMallocCoherent)
     uint32_t* count = nullptr;  // device counter, zero between launches
     uint32_t seq = 0;
     bool armed = false, taken = false;
 };
-F32Signal g_f32_signal;
+thread_local F32Signal g_f32_signal;
 
 }  // namespace pyc
 
