@@ -63,9 +63,9 @@ int pyc_hip_w8a16_chain_supported(int M, int nsteps, const int* N, const int* K)
 int pyc_hip_w8a16_chain_error_enqueue(int* host_dst, void* stream);
 /* completion word of a run (run_signal.hip) */
 int pyc_hip_run_signal_enqueue(uint32_t* host_word, uint32_t seq, void* stream);
-/* the fp32 GEMM's own completion store (gemm_f32.hip) */
-void pyc_hip_gemm_f32_signal_arm(uint32_t* host_word, uint32_t* dev_count, uint32_t seq);
-int pyc_hip_gemm_f32_signal_taken(void);
+/* the completion store by the run's last kernel itself (run_signal.hip) */
+void pyc_hip_run_signal_arm(uint32_t* host_word, uint32_t* dev_count, uint32_t seq);
+int pyc_hip_run_signal_taken(void);
 /* 1 when a GEMM symbol takes alpha = 1, beta = 0 only; 1 when it names the
  * persistent kernel alone, which refuses beta != 0 and unaligned C or bias
  * (hip_kernels.c) */
@@ -920,7 +920,7 @@ static int ws_init(void) {
     }
     *g_ws.done_word = 0;
     g_ws.done_seq = 0;
-    /* the signalling kernel's counters: 9 x 256 bytes (gemm_f32.hip) */
+    /* the signalling kernels' counters: 9 x 256 bytes (run_signal_arrive) */
     if (hipMalloc((void**)&g_ws.done_count, 4096) != hipSuccess) {
         g_ws.done_count = NULL;
         return -1;
@@ -1073,12 +1073,11 @@ static uint64_t fnv(uint64_t h, const void* p, size_t n) {
     return h;
 }
 
-/* Enqueue the kernels of the plan on the workspace stream; vp[v] is the
- * device storage of value v (workspace, or the caller's device tensor). */
-/* Enqueues the plan's kernels on the backend stream. arm_seq != 0: the run's
- * last kernel is also its last work on the stream, and when that kernel can
- * store the completion word itself (the fp32 LDS-DMA GEMM) it is launched so;
- * *signalled says whether it was. */
+/* Enqueues the plan's kernels on the backend stream; vp[v] is the device
+ * storage of value v (workspace, or the caller's device tensor). arm_seq != 0:
+ * the run's last kernel is also its last work on the stream, and when that
+ * kernel can store the completion word itself (the fp32 LDS-DMA GEMM) it is
+ * launched so; *signalled says whether it was. */
 static int enqueue_steps(const pyc_ir_module* m, const hip_plan* plan, void* const* vp, uint32_t arm_seq,
                          int* signalled, char* why, size_t why_cap) {
     size_t s;
@@ -1088,7 +1087,7 @@ static int enqueue_steps(const pyc_ir_module* m, const hip_plan* plan, void* con
         const hip_step* st = &plan->steps[s];
         void* out = vp[st->out];
         const size_t clen = (size_t)st->chain_len;
-        const int arm = arm_seq != 0 && s + 1 == plan->nsteps && st->kind == ST_GEMM && st->dtype == PYC_DTYPE_F32;
+        const int arm = arm_seq != 0 && s + 1 == plan->nsteps && st->kind == ST_GEMM;
         if (clen >= 2) {
             /* the whole run of fp8-weight steps in one launch */
             const void* wq[HIP_CHAIN_MAX_STEPS];
@@ -1133,7 +1132,7 @@ static int enqueue_steps(const pyc_ir_module* m, const hip_plan* plan, void* con
             beta = 1.0f;
         }
         if (arm) {
-            pyc_hip_gemm_f32_signal_arm(g_ws.done_word, g_ws.done_count, arm_seq);
+            pyc_hip_run_signal_arm(g_ws.done_word, g_ws.done_count, arm_seq);
         }
         switch (st->kind) {
             case ST_GEMM:
@@ -1176,7 +1175,7 @@ static int enqueue_steps(const pyc_ir_module* m, const hip_plan* plan, void* con
                 break;
         }
         if (arm) {
-            *signalled = pyc_hip_gemm_f32_signal_taken() && rc == 0;
+            *signalled = pyc_hip_run_signal_taken() && rc == 0;
         }
         if (rc != 0) {
             snprintf(why, why_cap, "hip_kernel_failed:%s", st->symbol);

@@ -55,4 +55,40 @@ __device__ inline f32x4 mfma16x16x32(const u32x4& a, const u32x4& b, const f32x4
 
 __device__ inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
+// Completion word of a synchronous run (run_signal.hip). The run path arms it
+// for its last kernel; a launcher whose kernel can store it itself claims it
+// (per thread) and launches that kernel's signalling form.
+struct RunSignal {
+    uint32_t* word;   // pinned, host-coherent word the host spins on
+    uint32_t* count;  // device counters (9 x 256 bytes), zero between launches
+    uint32_t seq;     // value to store
+};
+bool run_signal_claim(RunSignal* out);
+constexpr int kRunSignalPad = 64;  // counters 256 bytes apart: the top one, then one per group
+
+// Thread 0 of each workgroup of a 1-D grid, once the workgroup's results have
+// reached the coherent level (agent-scope stores, then vmcnt(0) and a
+// workgroup barrier): counts the workgroup in, two-level so that a grid that
+// finishes at once does not queue every arrival on one counter (workgroup b
+// in group b % 8, the XCD it was dispatched to; each group's last arrival in
+// the top counter). The last arrival re-arms the counters (the next launch
+// follows this kernel's end in stream order) and stores the sequence number.
+// The results are complete by then (every arrival followed its workgroup's
+// completed stores, and this store depends on the last arrival's result), so
+// the word's store needs no release fence, whose L2 write-back would only
+// delay it.
+__device__ inline void run_signal_arrive(uint32_t* count, uint32_t* word, uint32_t seq) {
+    const uint32_t g = blockIdx.x & 7, G = gridDim.x;
+    const uint32_t in_g = (G >> 3) + (g < (G & 7) ? 1u : 0u);
+    uint32_t* gc = count + (1 + g) * kRunSignalPad;
+    if (__hip_atomic_fetch_add(gc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == in_g - 1) {
+        __hip_atomic_store(gc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t groups = G < 8 ? G : 8u;
+        if (__hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == groups - 1) {
+            __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(word, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+    }
+}
+
 }  // namespace pyc

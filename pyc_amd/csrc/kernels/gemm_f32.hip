@@ -202,18 +202,15 @@ gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ B, float*
 // lanes of each k slot read 16 consecutive n of rows 4 apart, which the
 // swizzle puts in four different 16-bank groups.
 constexpr int kF32Stages = 4;
-// completion counters of the signalling launch: the top one, then one per XCD
-// group, 256 bytes apart (the device buffer holds 9 x 256 bytes)
-constexpr int kF32SigPad = 64;
 constexpr size_t kF32DmaLds = (size_t)kF32Stages * 2 * kF32BM * kF32BK * 4;
 
 // SIG: the launch ends a synchronous run, and the kernel itself tells the host
 // when its results are complete (instead of a separate one-lane kernel behind
 // it on the stream). C is stored with agent-scope stores, which write through
 // the XCD's L2 to the coherent level; once a workgroup's stores have completed
-// its thread 0 counts it in `done_count`, and the last workgroup re-arms the
-// counters and stores `done_seq` into the pinned host word (a system-scope
-// store). A kernel on any stream that the host starts after seeing the word
+// its thread 0 counts it in `done_count` (run_signal_arrive), and the last
+// arrival re-arms the counters and stores `done_seq` into the pinned host
+// word. A kernel on any stream that the host starts after seeing the word
 // reads the whole of C, although the grid's last waves may still be exiting.
 template <bool BT, bool SIG>
 __global__ void __launch_bounds__(512, 1)
@@ -394,63 +391,11 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
     if constexpr (SIG) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's part of C reached the coherent level
         __syncthreads();
-        if (tid == 0) {
-            // two-level count: the workgroups finish together, and 256
-            // arrivals on one counter queue behind each other. Workgroup b
-            // counts in group b % 8 (the XCD it was dispatched to); the
-            // group's last arrival counts in the top counter.
-            const uint32_t g = blockIdx.x & 7, G = gridDim.x;
-            const uint32_t in_g = (G >> 3) + (g < (G & 7) ? 1u : 0u);
-            uint32_t* gc = done_count + (1 + g) * kF32SigPad;
-            if (__hip_atomic_fetch_add(gc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == in_g - 1) {
-                __hip_atomic_store(gc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                const uint32_t groups = G < 8 ? G : 8u;
-                if (__hip_atomic_fetch_add(done_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == groups - 1) {
-                    // every workgroup's C is complete: re-arm for the next
-                    // launch (stream order puts it after this kernel's end),
-                    // then publish the run's sequence number. C has reached
-                    // the coherent level already (each arrival followed its
-                    // workgroup's completed write-through stores, and this
-                    // store depends on the last arrival's result), so the
-                    // store needs no release fence, whose L2 write-back would
-                    // only delay it.
-                    __hip_atomic_store(done_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    __hip_atomic_store(done_word, done_seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                }
-            }
-        }
+        if (tid == 0) run_signal_arrive(done_count, done_word, done_seq);
     }
 }
 
-// Completion signal armed by the run path for its last kernel: the next
-// LDS-DMA launch on the same thread carries it, and the run asks afterwards
-// whether one did. Per thread, so that a GEMM another thread dispatches
-// meanwhile cannot take it.
-struct F32Signal {
-    uint32_t* word = nullptr;   // pinned host word (hipHostMallocCoherent)
-    uint32_t* count = nullptr;  // device counter, zero between launches
-    uint32_t seq = 0;
-    bool armed = false, taken = false;
-};
-thread_local F32Signal g_f32_signal;
-
 }  // namespace pyc
-
-extern "C" void pyc_hip_gemm_f32_signal_arm(uint32_t* host_word, uint32_t* dev_count, uint32_t seq) {
-    pyc::g_f32_signal.word = host_word;
-    pyc::g_f32_signal.count = dev_count;
-    pyc::g_f32_signal.seq = seq;
-    pyc::g_f32_signal.armed = host_word != nullptr && dev_count != nullptr;
-    pyc::g_f32_signal.taken = false;
-}
-
-// 1 when a launch since the arm carried the signal; disarms either way.
-extern "C" int pyc_hip_gemm_f32_signal_taken(void) {
-    const int t = pyc::g_f32_signal.taken ? 1 : 0;
-    pyc::g_f32_signal.armed = false;
-    pyc::g_f32_signal.taken = false;
-    return t;
-}
 
 extern "C" int pyc_hip_gemm_f32_launch(int b_trans, int M, int N, int K, const void* A,
                                        const void* B, void* C, float alpha, float beta,
@@ -469,11 +414,9 @@ extern "C" int pyc_hip_gemm_f32_launch(int b_trans, int M, int N, int K, const v
     if (dma) {
         const dim3 tiles((unsigned)((M / kF32BM) * (N / kF32BN)));
         const int gm = M / kF32BM < 4 ? M / kF32BM : 4;
-        if (g_f32_signal.armed) {
+        RunSignal sg;
+        if (run_signal_claim(&sg)) {
             // this launch ends the run: it stores the completion word itself
-            const F32Signal sg = g_f32_signal;
-            g_f32_signal.armed = false;
-            g_f32_signal.taken = true;
             if (b_trans)
                 hipLaunchKernelGGL((gemm_f32_dma_kernel<true, true>), tiles, block, 0, s, a, b, c, M, N, K, alpha,
                                    beta, bias, epi, gm, sg.word, sg.count, sg.seq);

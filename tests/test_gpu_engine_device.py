@@ -132,6 +132,49 @@ def test_device_tensors_back_to_back_runs_read_at_once(gpu, M, K, N):
     mdl.close()
 
 
+@pytest.mark.parametrize("M,K,N", [(512, 512, 512), (200, 128, 72), (2048, 2048, 2048)])
+def test_device_tensors_back_to_back_runs_bf16(gpu, M, K, N):
+    """The bf16 form of the test above (these GEMMs end on the one-lane
+    kernel's completion word): 512^3, a ragged 200x128x72 and 2048^3. Each
+    run's output is read on the default stream as soon as the call returns;
+    bit for bit against the host-buffer run of the same inputs, and the first
+    case within 2e-2 of max|ref| of the oracle."""
+    torch = gpu
+    r = np.random.default_rng(11)
+    mdl = _gemm_module(M, K, N, dtype=abi.DTYPE_BF16)
+    assert mdl.status == 0
+    cases = []
+    for _ in range(3):
+        a = oracle.f32_to_bf16((r.standard_normal((M, K)) / 16).astype(np.float32))
+        w = oracle.f32_to_bf16(r.standard_normal((K, N)).astype(np.float32))
+        b = oracle.f32_to_bf16(r.standard_normal(N).astype(np.float32))
+        st, (ref,), s = mdl.run([a, w, b], [(M, N)], in_dtypes=[abi.DTYPE_BF16] * 3, out_dtypes=[abi.DTYPE_BF16],
+                                out_np_dtype=np.uint16)
+        assert st == 0, s.execution_path
+        cases.append(([torch.from_numpy(t.view(np.int16)).cuda() for t in (a, w, b)], ref.copy(), (a, w, b)))
+    a, w, b = cases[0][2]
+    oref = np.maximum(oracle.gemm_bf16(a, w, False, threads=8) + oracle.bf16_to_f32(b)[None, :], 0.0)
+    assert rel_max_err(oracle.bf16_to_f32(cases[0][1]), oref) <= 2e-2
+    X, W, Bv = (torch.empty_like(t) for t in cases[0][0])
+    Y = torch.zeros((M, N), dtype=torch.int16, device="cuda")
+    got = []
+    torch.cuda.synchronize()
+    for i in range(12):
+        x, w_, b_ = cases[i % 3][0]
+        X.copy_(x)
+        W.copy_(w_)
+        Bv.copy_(b_)
+        rc, s = _run(mdl, [_dt(X, abi.DTYPE_BF16), _dt(W, abi.DTYPE_BF16), _dt(Bv, abi.DTYPE_BF16)],
+                     [_dt(Y, abi.DTYPE_BF16)])
+        assert rc == 0, s.execution_path
+        assert s.execution_path.decode().startswith("hip_native:"), s.execution_path
+        got.append(Y.clone())
+    torch.cuda.synchronize()
+    for i, g in enumerate(got):
+        assert np.array_equal(g.cpu().numpy().view(np.uint16), cases[i % 3][1]), f"run {i}"
+    mdl.close()
+
+
 def test_device_tensors_rebind_and_mixed(gpu):
     """New device addresses capture a new graph (a graph bakes in the addresses
     it was captured with); host and device tensors in one call; a host run
