@@ -84,9 +84,13 @@ def build(verbose: bool = True, jobs: int | None = None) -> str:
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(_run, cmds))
     tmp = LIB_PATH + ".tmp"
+    # the full library resolves every symbol itself (-z defs: an entry point
+    # missing from the sources fails the link, not a later load); the
+    # backend-only one below takes the registry calls from the engine it is
+    # loaded under
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp,
           *[_obj(s) for s in hip + c], "-L", os.path.join(ROCM, "lib"), "-lamdhip64",
-          "-lpthread", "-lm", "-Wl,-Bsymbolic", f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}"])
+          "-lpthread", "-lm", "-Wl,-Bsymbolic", "-Wl,-z,defs", f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}"])
     shutil.move(tmp, LIB_PATH)
     tmp = BACKEND_LIB_PATH + ".tmp"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp,
