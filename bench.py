@@ -616,9 +616,9 @@ def wl_engine_cfg1(torch, args):
                      "traffic": load_traffic("gemm_f32_cfg1"), "kernel_ms": kernel_ms},
         "latency_ms": eng.pop("latency_ms"),
         "engine": eng,
-        # BASELINE.md's one published number for this metric: fp32 GEMM 1024^3
-        # via pyc_run_model, 28.3142 TFLOP/s (RTX 6000 Ada, cuBLASLt, TF32 by
-        # default); this run is true fp32 plus the bias+ReLU epilogue
+        # the reference's one published number for this metric: fp32 GEMM
+        # 1024^3 via pyc_run_model, 28.3142 TFLOP/s (RTX 6000 Ada, cuBLASLt,
+        # TF32 by default); this run is true fp32 plus the bias+ReLU epilogue
         "vs_baseline": flops / (ms_step * 1e-3) / 1e12 / 28.3142,
         "baseline_ref": "28.3142 TFLOP/s, fp32(TF32) 1024^3 via pyc_run_model, RTX 6000 Ada "
                         "(reference docs/reports/ada-box-technical-breakdown-2026-04-04.md:118)",
