@@ -175,6 +175,53 @@ def test_device_tensors_back_to_back_runs_bf16(gpu, M, K, N):
     mdl.close()
 
 
+def test_device_runs_alternate_completion_paths(gpu):
+    """Two models called in turn, 16 times each: an fp32 1024^3 GEMM, whose
+    kernel stores the run's completion word itself, and a bf16 512^3 GEMM,
+    which ends on the one-lane kernel. Both share the backend's sequence
+    number and counters; each output is read on the default stream as soon as
+    its call returns and must equal its host-buffer run bit for bit."""
+    torch = gpu
+    r = np.random.default_rng(5)
+    f32 = _gemm_module(1024, 1024, 1024)
+    b16 = _gemm_module(512, 512, 512, dtype=abi.DTYPE_BF16)
+    assert f32.status == 0 and b16.status == 0
+    x, w = (r.uniform(-1, 1, (1024, 1024)).astype(np.float32) for _ in range(2))
+    b = r.uniform(-1, 1, 1024).astype(np.float32)
+    st, (ref32,), _ = f32.run([x, w, b], [(1024, 1024)])
+    assert st == 0
+    a16 = oracle.f32_to_bf16((r.standard_normal((512, 512)) / 16).astype(np.float32))
+    w16 = oracle.f32_to_bf16(r.standard_normal((512, 512)).astype(np.float32))
+    b16v = oracle.f32_to_bf16(r.standard_normal(512).astype(np.float32))
+    st, (ref16,), _ = b16.run([a16, w16, b16v], [(512, 512)], in_dtypes=[abi.DTYPE_BF16] * 3,
+                              out_dtypes=[abi.DTYPE_BF16], out_np_dtype=np.uint16)
+    assert st == 0
+    X, W, Bv = (torch.from_numpy(t).cuda() for t in (x, w, b))
+    A16, W16, B16 = (torch.from_numpy(t.view(np.int16)).cuda() for t in (a16, w16, b16v))
+    Y32 = torch.full((1024, 1024), float("nan"), device="cuda")
+    Y16 = torch.zeros((512, 512), dtype=torch.int16, device="cuda")
+    got32, got16 = [], []
+    torch.cuda.synchronize()
+    for _ in range(16):
+        Y32.fill_(float("nan"))
+        rc, s = _run(f32, [_dt(X, abi.DTYPE_F32), _dt(W, abi.DTYPE_F32), _dt(Bv, abi.DTYPE_F32)],
+                     [_dt(Y32, abi.DTYPE_F32)])
+        assert rc == 0, s.execution_path
+        got32.append(Y32.clone())
+        Y16.zero_()
+        rc, s = _run(b16, [_dt(A16, abi.DTYPE_BF16), _dt(W16, abi.DTYPE_BF16), _dt(B16, abi.DTYPE_BF16)],
+                     [_dt(Y16, abi.DTYPE_BF16)])
+        assert rc == 0, s.execution_path
+        got16.append(Y16.clone())
+    torch.cuda.synchronize()
+    for i in range(16):
+        assert np.array_equal(got32[i].cpu().numpy(), ref32), f"fp32 run {i}"
+        assert np.array_equal(got16[i].cpu().numpy().view(np.uint16), ref16), f"bf16 run {i}"
+    assert rel_max_err(ref32, oracle.gemm_bias_relu_f32(x, w, b, relu=True, threads=8)) <= 1e-4
+    f32.close()
+    b16.close()
+
+
 def test_device_tensors_rebind_and_mixed(gpu):
     """New device addresses capture a new graph (a graph bakes in the addresses
     it was captured with); host and device tensors in one call; a host run
